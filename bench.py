@@ -1,0 +1,270 @@
+"""Benchmark of the quantized-matmul hot path on one MI355X.
+
+Headline (BASELINE.json metric "4-bit qmatmul: decode GEMV HBM GB/s (%peak);
+prefill TFLOP/s (%MFMA peak)"):
+
+* value    = decode GEMV HBM GB/s: affine 4-bit gs64, K=4096, N=14336, M=1,
+             bf16 x/scales/biases.  A "step" is one GEMV over each of a pool
+             of distinct weight sets (> 2x the 256 MB Infinity Cache, so every
+             launch streams from HBM), replayed from a HIP graph.
+* prefill  = the prefill GEMM (M=2048, K=4096, N=14336, bf16) in TFLOP/s.
+* roofline = the GEMV kernel's algorithmic bytes per launch / its average
+             launch duration (HIP events around each launch on the stream the
+             kernel runs on) against 8 TB/s; prefill likewise against the
+             2.5 PFLOP/s bf16 dense MFMA peak.
+* cpu_baseline = the CPU restatement of the same GEMV (oracle/, OpenMP)
+             timed on this host on a bounded sample.
+
+Inputs are synthetic (seeded), resident in HBM before timing starts.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, TFLOP/s
+
+
+def gemv_bytes(M, N, K, bits=4, gs=64, xbytes=2, sbytes=2):
+    """Algorithmic bytes of one quantized GEMV: packed weight + scales + biases
+    + x + out."""
+    return N * K * bits // 8 + 2 * N * (K // gs) * sbytes + M * K * xbytes + M * N * xbytes
+
+
+def make_weight(ops, N, K, gen, dt=torch.bfloat16, gs=64, bits=4):
+    """Random packed codes + scales/biases at the scale of a quantized N(0,0.02)
+    weight (quantize() of a full fp matrix per set would dominate set-up)."""
+    words = torch.randint(-2**31, 2**31 - 1, (N, K * bits // 32), generator=gen, device="cuda",
+                          dtype=torch.int32).view(torch.uint32)
+    s = (torch.rand((N, K // gs), generator=gen, device="cuda") * 0.004 + 0.002).to(dt)
+    b = (torch.randn((N, K // gs), generator=gen, device="cuda") * 0.02).to(dt)
+    return words, s, b
+
+
+def time_launches(fn, n, stream):
+    """Average device duration of `fn` over n launches, events bracketing each
+    launch on `stream` (the stream the kernel is enqueued on)."""
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(n)]
+    for a, b in evs:
+        a.record(stream)
+        fn()
+        b.record(stream)
+    torch.cuda.synchronize()
+    return sum(a.elapsed_time(b) for a, b in evs) / n * 1e-3
+
+
+def bench_gemv(ops, steps, warmup, M=1, N=14336, K=4096, pool_bytes=640 << 20):
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    per = gemv_bytes(M, N, K)
+    P = max(2, int(np.ceil(pool_bytes / per)))
+    pool = [make_weight(ops, N, K, gen) for _ in range(P)]
+    x = torch.randn((M, K), generator=gen, device="cuda").to(torch.bfloat16)
+    stream = torch.cuda.current_stream()
+    outs = [None] * P
+
+    def one_pass():
+        for i, (w, s, b) in enumerate(pool):
+            outs[i] = ops.quantized_matmul(x, w, s, b, True, 64, 4, "affine")
+
+    one_pass()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        one_pass()
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for _ in range(steps):
+        g.replay()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    total_s = t0.elapsed_time(t1) * 1e-3
+    # per-launch kernel durations, eager, rotating through the pool
+    it = iter(range(10 ** 9))
+    def launch():
+        i = next(it) % P
+        w, s, b = pool[i]
+        ops.quantized_matmul(x, w, s, b, True, 64, 4, "affine")
+    avg_launch_s = time_launches(launch, 4 * P, stream)
+    res = {
+        "gbs": per * P * steps / total_s / 1e9,
+        "ms_per_step": total_s / steps * 1e3,
+        "bytes_per_launch": per,
+        "pool_sets": P,
+        "avg_launch_us": avg_launch_s * 1e6,
+        "kernel_gbs": per / avg_launch_s / 1e9,
+    }
+    del pool, outs, g
+    torch.cuda.empty_cache()
+    return res
+
+
+def bench_prefill(ops, steps, warmup, M=2048, N=14336, K=4096):
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    w, s, b = make_weight(ops, N, K, gen)
+    x = torch.randn((M, K), generator=gen, device="cuda").to(torch.bfloat16)
+    stream = torch.cuda.current_stream()
+    fn = lambda: ops.quantized_matmul(x, w, s, b, True, 64, 4, "affine")  # noqa: E731
+    for _ in range(max(1, warmup)):
+        fn()
+    torch.cuda.synchronize()
+    n = max(3, steps)
+    avg = time_launches(fn, n, stream)
+    flops = 2.0 * M * N * K
+    return {"tflops": flops / avg / 1e12, "avg_launch_us": avg * 1e6, "flops_per_launch": flops}
+
+
+def bench_llama_decode(ops, Ms=(1, 4, 8, 16, 32), steps=5):
+    """Llama-3-8B-shaped decode step: 32 layers x {q,k,v,o,gate,up,down} of
+    distinct 4-bit gs64 weights; tokens/s = M / step time."""
+    shapes = [(4096, 4096), (1024, 4096), (1024, 4096), (4096, 4096), (14336, 4096),
+              (14336, 4096), (4096, 14336)]
+    gen = torch.Generator(device="cuda").manual_seed(2)
+    layers = [[make_weight(ops, N, K, gen) for (N, K) in shapes] for _ in range(32)]
+    wbytes = sum(w.numel() * 4 + s.numel() * 2 * 2 for L in layers for (w, s, b) in L)
+    out = {}
+    stream = torch.cuda.current_stream()
+    for M in Ms:
+        xs = {K: torch.randn((M, K), generator=gen, device="cuda").to(torch.bfloat16)
+              for K in (4096, 14336)}
+
+        def step():
+            for L in layers:
+                for (w, s, b), (N, K) in zip(L, shapes):
+                    ops.quantized_matmul(xs[K], w, s, b, True, 64, 4, "affine")
+
+        step()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            step()
+        g.replay()
+        torch.cuda.synchronize()
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record(stream)
+        for _ in range(steps):
+            g.replay()
+        t1.record(stream)
+        torch.cuda.synchronize()
+        dt = t0.elapsed_time(t1) * 1e-3 / steps
+        out[str(M)] = {"ms_per_step": dt * 1e3, "tokens_per_s": M / dt,
+                       "weight_gbs": wbytes / dt / 1e9}
+        del g
+    del layers
+    torch.cuda.empty_cache()
+    return out
+
+
+def cpu_baseline(seconds=10.0, N=14336, K=4096):
+    """The oracle's streaming GEMV (oracle/iqmm_oracle.c iqo_qmv_affine) on the
+    host, same shape as the headline; bounded sample of ~`seconds`."""
+    import oracle
+    threads = min(16, os.cpu_count() or 1)
+    rng = np.random.default_rng(0)
+    w = rng.integers(0, 2**32, (N, K // 8), dtype=np.uint64).astype(np.uint32)
+    s = oracle.from_float((rng.random((N, K // 64)) * 0.004 + 0.002).astype(np.float32), "bf16")
+    b = oracle.from_float((rng.standard_normal((N, K // 64)) * 0.02).astype(np.float32), "bf16")
+    x = oracle.from_float(rng.standard_normal((1, K)).astype(np.float32), "bf16")
+    for _ in range(2):
+        oracle.qmv_affine(x, "bf16", w, s, b, "bf16", 64, 4, nthreads=threads)
+    times = []
+    t_end = time.perf_counter() + seconds
+    while len(times) < 5 or time.perf_counter() < t_end:
+        t = time.perf_counter()
+        oracle.qmv_affine(x, "bf16", w, s, b, "bf16", 64, 4, nthreads=threads)
+        times.append(time.perf_counter() - t)
+        if len(times) >= 200:
+            break
+    med = float(np.median(times))
+    return {"value": gemv_bytes(1, N, K) / med / 1e9, "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": f"{len(times)} GEMVs K={K} N={N} M=1 q4 gs64 bf16 (median "
+                      f"{med * 1e3:.1f} ms) by the oracle's OpenMP streaming qmv"}
+
+
+def load_traffic():
+    p = os.path.join(ROOT, "profiles", "traffic.json")
+    if os.path.exists(p):
+        with open(p) as f:
+            return json.load(f)
+    return {}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-llama", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path "
+              f"(asked for --gpus {args.gpus}).", file=sys.stderr)
+        sys.exit(2)
+    if int(os.environ.get("RANK", "0")) != 0:
+        return
+    from ironmlx_amd import ops, _lib
+    _lib.load()
+    torch.cuda.set_device(0)
+
+    gemv = bench_gemv(ops, args.steps, args.warmup)
+    prefill = bench_prefill(ops, args.steps, args.warmup)
+    llama = None if args.no_llama else bench_llama_decode(ops)
+    traffic = load_traffic().get("gemv_q4_gs64_k4096_n14336_m1")
+    line = {
+        "metric": "4-bit qmatmul: decode GEMV HBM GB/s (%peak); prefill TFLOP/s (%MFMA peak)",
+        "value": round(gemv["gbs"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(gemv["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded random 4-bit codes, bf16 scales/biases, x~N(0,1))",
+        "config": {"workload": "decode GEMV affine q4 gs64 K=4096 N=14336 M=1 bf16, "
+                               f"{gemv['pool_sets']} distinct weight sets per step "
+                               "(HIP-graph replay)",
+                   "K": 4096, "N": 14336, "M": 1, "group_size": 64, "bits": 4,
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(gemv["kernel_gbs"], 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gemv["kernel_gbs"] / HBM_PEAK_GBS, 4),
+                     "traffic": traffic,
+                     "bytes_per_launch": gemv["bytes_per_launch"],
+                     "avg_launch_us": round(gemv["avg_launch_us"], 3)},
+        "prefill": {"workload": "prefill GEMM affine q4 gs64 M=2048 K=4096 N=14336 bf16",
+                    "value": round(prefill["tflops"], 2), "unit": "TFLOP/s",
+                    "roofline": {"bound": "mfma", "achieved": round(prefill["tflops"], 2),
+                                 "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                 "frac": round(prefill["tflops"] / BF16_PEAK_TFLOPS, 4),
+                                 "avg_launch_us": round(prefill["avg_launch_us"], 2)}},
+    }
+    if llama is not None:
+        line["llama3_8b_decode"] = llama
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

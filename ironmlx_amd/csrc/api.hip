@@ -1,0 +1,447 @@
+// api.hip — the C ABI (include/iqmm.h): argument validation, shape inference
+// and kernel dispatch.
+//
+// Validation mirrors what mlx-c's quantized ops reject so that callers see the
+// same failures the Rust wrappers turn into Error::Mlx (mlx/src/error.rs:27-35):
+// unknown mode, unsupported bits / group size, dtype mismatches, shapes whose
+// packed width does not match K, scales of the wrong shape, missing or
+// unexpected biases, and batch shapes that do not broadcast.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+#include <vector>
+
+#include "../../include/iqmm.h"
+#include "launch.h"
+
+namespace iqmm {
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return 1;
+}
+
+int hip_fail(const char* op, hipError_t e) {
+  return fail("[%s] HIP error: %s", op, hipGetErrorString(e));
+}
+
+bool present(const iqmm_array& a) { return a.data != nullptr || a.ndim > 0; }
+
+bool is_float(int dt) { return dt == IQMM_FLOAT32 || dt == IQMM_FLOAT16 || dt == IQMM_BFLOAT16; }
+bool is_index(int dt) { return dt == IQMM_INT32 || dt == IQMM_UINT32 || dt == IQMM_INT64; }
+
+const char* dt_name(int dt) {
+  switch (dt) {
+    case IQMM_FLOAT32: return "float32";
+    case IQMM_FLOAT16: return "float16";
+    case IQMM_BFLOAT16: return "bfloat16";
+    case IQMM_UINT32: return "uint32";
+    case IQMM_UINT8: return "uint8";
+    case IQMM_INT32: return "int32";
+    case IQMM_INT64: return "int64";
+  }
+  return "unknown";
+}
+
+int64_t numel(const iqmm_array& a) {
+  int64_t n = 1;
+  for (int i = 0; i < a.ndim; ++i) n *= a.shape[i];
+  return n;
+}
+
+std::string shape_str(const iqmm_array& a) {
+  std::string s = "(";
+  for (int i = 0; i < a.ndim; ++i) {
+    s += std::to_string(a.shape[i]);
+    if (i + 1 < a.ndim) s += ",";
+  }
+  return s + ")";
+}
+
+struct QParams {
+  int mode, gs, bits;
+};
+
+// mode string + optionals -> resolved (mode, gs, bits); MLX's defaults per mode
+int resolve(const char* op, const char* mode, iqmm_optional_int group_size, iqmm_optional_int bits,
+            QParams& q) {
+  if (!mode) mode = "affine";
+  int dgs, dbits;
+  if (!strcmp(mode, "affine")) { q.mode = AFFINE; dgs = 64; dbits = 4; }
+  else if (!strcmp(mode, "mxfp4")) { q.mode = MXFP4; dgs = 32; dbits = 4; }
+  else if (!strcmp(mode, "mxfp8")) { q.mode = MXFP8; dgs = 32; dbits = 8; }
+  else if (!strcmp(mode, "nvfp4")) { q.mode = NVFP4; dgs = 16; dbits = 4; }
+  else return fail("[%s] Invalid quantization mode '%s'.", op, mode);
+  q.gs = group_size.has_value ? group_size.value : dgs;
+  q.bits = bits.has_value ? bits.value : dbits;
+  if (q.mode == AFFINE) {
+    if (q.gs != 32 && q.gs != 64 && q.gs != 128)
+      return fail("[%s] The requested group size %d is not supported. The supported group sizes are 32, 64, and 128.", op, q.gs);
+    if (q.bits != 2 && q.bits != 3 && q.bits != 4 && q.bits != 5 && q.bits != 6 && q.bits != 8)
+      return fail("[%s] The requested number of bits %d is not supported. The supported bits are 2, 3, 4, 5, 6 and 8.", op, q.bits);
+  } else {
+    if (q.gs != dgs)
+      return fail("[%s] Quantization mode '%s' requires group_size %d (got %d).", op, mode, dgs, q.gs);
+    if (q.bits != dbits)
+      return fail("[%s] Quantization mode '%s' requires bits %d (got %d).", op, mode, dbits, q.bits);
+  }
+  return 0;
+}
+
+// scales / biases checks shared by every op; rows_shape = w.shape[:-1]
+int check_scales(const char* op, const QParams& q, const iqmm_array& w, const iqmm_array& s,
+                 const iqmm_array& b, int64_t groups_last, int* sdt_out) {
+  if (!present(s) || s.ndim != w.ndim)
+    return fail("[%s] scales must have the same number of dimensions as w (%d), got %s.", op, w.ndim, shape_str(s).c_str());
+  for (int i = 0; i + 1 < w.ndim; ++i)
+    if (s.shape[i] != w.shape[i])
+      return fail("[%s] Shape of scales %s does not match w %s.", op, shape_str(s).c_str(), shape_str(w).c_str());
+  if (s.shape[s.ndim - 1] != groups_last)
+    return fail("[%s] scales last dimension %lld does not match the expected number of groups %lld.", op,
+                (long long)s.shape[s.ndim - 1], (long long)groups_last);
+  if (q.mode == AFFINE) {
+    if (!is_float(s.dtype)) return fail("[%s] affine scales must be floating point, got %s.", op, dt_name(s.dtype));
+    if (!present(b)) return fail("[%s] Biases must be provided for affine quantization.", op);
+    if (b.dtype != s.dtype || b.ndim != s.ndim)
+      return fail("[%s] biases must have the same shape and dtype as scales.", op);
+    for (int i = 0; i < s.ndim; ++i)
+      if (b.shape[i] != s.shape[i]) return fail("[%s] biases must have the same shape and dtype as scales.", op);
+  } else {
+    if (s.dtype != IQMM_UINT8) return fail("[%s] Scales for mode with fp elements must be uint8, got %s.", op, dt_name(s.dtype));
+    if (present(b)) return fail("[%s] Biases must not be provided for quantization mode other than affine.", op);
+  }
+  *sdt_out = s.dtype;
+  return 0;
+}
+
+// right-aligned broadcast of two batch shapes; strides are in matrices
+int broadcast2(const char* op, const int64_t* a, int na, const int64_t* b, int nb, BatchMap& bm,
+               std::vector<int64_t>& out_shape) {
+  const int nd = na > nb ? na : nb;
+  if (nd > 8) return fail("[%s] too many batch dimensions (%d).", op, nd);
+  out_shape.assign(nd, 1);
+  int64_t sa = 1, sb = 1;
+  std::vector<int64_t> sta(nd, 0), stb(nd, 0);
+  for (int d = nd - 1; d >= 0; --d) {
+    const int ia = d - (nd - na), ib = d - (nd - nb);
+    const int64_t da = ia >= 0 ? a[ia] : 1, db = ib >= 0 ? b[ib] : 1;
+    if (da != db && da != 1 && db != 1)
+      return fail("[%s] Shapes cannot be broadcast: batch dims do not match.", op);
+    out_shape[d] = da == 1 ? db : da;
+    sta[d] = da == 1 ? 0 : sa;
+    stb[d] = db == 1 ? 0 : sb;
+    sa *= da;
+    sb *= db;
+  }
+  bm.ndim = nd;
+  for (int d = 0; d < nd; ++d) {
+    bm.shape[d] = out_shape[d];
+    bm.xs[d] = sta[d];
+    bm.ws[d] = stb[d];
+  }
+  return 0;
+}
+
+int set_or_check_res(const char* op, iqmm_array* res, const std::vector<int64_t>& shape, int dtype,
+                     bool* query) {
+  if (!res) return fail("[%s] result pointer is null.", op);
+  if ((int)shape.size() > IQMM_MAX_NDIM) return fail("[%s] result has too many dimensions.", op);
+  if (res->data == nullptr) {
+    res->ndim = static_cast<int32_t>(shape.size());
+    for (size_t i = 0; i < shape.size(); ++i) res->shape[i] = shape[i];
+    res->dtype = dtype;
+    *query = true;
+    return 0;
+  }
+  *query = false;
+  bool okk = res->ndim == (int)shape.size() && res->dtype == dtype;
+  for (size_t i = 0; okk && i < shape.size(); ++i) okk = res->shape[i] == shape[i];
+  if (!okk) {
+    std::string want = "(";
+    for (size_t i = 0; i < shape.size(); ++i) want += std::to_string(shape[i]) + (i + 1 < shape.size() ? "," : "");
+    want += ")";
+    return fail("[%s] result buffer is %s %s but the op produces %s %s.", op, shape_str(*res).c_str(),
+                dt_name(res->dtype), want.c_str(), dt_name(dtype));
+  }
+  return 0;
+}
+
+__global__ void fill_kernel(uint16_t* p16, float* p32, int64_t n, uint16_t v16, float v32) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i < n) {
+    if (p16) p16[i] = v16;
+    else p32[i] = v32;
+  }
+}
+
+hipError_t fill_zero(void* p, int dt, int64_t n, hipStream_t st) {
+  if (n == 0) return hipSuccess;
+  const int64_t nb = (n + 255) / 256;
+  hipLaunchKernelGGL(fill_kernel, dim3(static_cast<unsigned>(nb)), dim3(256), 0, st,
+                     dt == IQMM_FLOAT32 ? nullptr : static_cast<uint16_t*>(p),
+                     dt == IQMM_FLOAT32 ? static_cast<float*>(p) : nullptr, n, uint16_t(0), 0.f);
+  return hipGetLastError();
+}
+
+// choose the kernel family for one problem
+hipError_t run_qmm(QmmArgs& a) {
+  const bool small_m = a.M <= 8;
+  if (!small_m && qmm_mfma_supported(a)) return launch_qmm_mfma(a);
+  return a.transpose ? launch_qmv(a) : launch_qvm(a);
+}
+
+// common core of quantized_matmul / gather_qmm once batch mapping is known
+int qmm_common(const char* op, iqmm_array* res, const iqmm_array& x, const iqmm_array& w,
+               const iqmm_array& s, const iqmm_array& b, bool transpose, const QParams& q,
+               int64_t& M, int64_t& N, int64_t& K, int* sdt) {
+  if (!present(x) || x.ndim < 1) return fail("[%s] x must have at least one dimension.", op);
+  if (!is_float(x.dtype)) return fail("[%s] Only real floating types are supported but x.dtype() == %s.", op, dt_name(x.dtype));
+  if (!present(w) || w.ndim < 2) return fail("[%s] The quantized weight should be at least 2D but received %s.", op, shape_str(w).c_str());
+  if (w.dtype != IQMM_UINT32) return fail("[%s] The weight matrix should be uint32 but received %s.", op, dt_name(w.dtype));
+  K = x.shape[x.ndim - 1];
+  M = x.ndim >= 2 ? x.shape[x.ndim - 2] : 1;
+  const int64_t wlast = w.shape[w.ndim - 1], wrows = w.shape[w.ndim - 2];
+  if ((wlast * 32) % q.bits != 0)
+    return fail("[%s] packed width %lld is not a whole number of %d-bit codes.", op, (long long)wlast, q.bits);
+  const int64_t unpacked = wlast * 32 / q.bits;
+  if (transpose) {
+    if (unpacked != K)
+      return fail("[%s] Last dimension of first input with shape (..., %lld) must be equal to the unpacked last dimension of the quantized weight (%lld).",
+                  op, (long long)K, (long long)unpacked);
+    N = wrows;
+    if (K % q.gs != 0) return fail("[%s] K=%lld is not divisible by group_size %d.", op, (long long)K, q.gs);
+    if (check_scales(op, q, w, s, b, K / q.gs, sdt)) return 1;
+  } else {
+    if (wrows != K)
+      return fail("[%s] Last dimension of first input with shape (..., %lld) must be equal to the second-to-last dimension of the weight (%lld).",
+                  op, (long long)K, (long long)wrows);
+    N = unpacked;
+    if (N % q.gs != 0) return fail("[%s] N=%lld is not divisible by group_size %d.", op, (long long)N, q.gs);
+    if (check_scales(op, q, w, s, b, N / q.gs, sdt)) return 1;
+    if (N % 32 != 0) return fail("[%s] transpose=false requires the output width (%lld) to be a multiple of 32.", op, (long long)N);
+  }
+  if (q.mode == AFFINE && *sdt != x.dtype)
+    return fail("[%s] x (%s) and scales (%s) must have the same dtype.", op, dt_name(x.dtype), dt_name(*sdt));
+  if (K % 32 != 0) return fail("[%s] The reduction dimension K=%lld must be a multiple of 32.", op, (long long)K);
+  if (M > 0x7fffffffLL || N > 0x7fffffffLL || K > 0x7fffffffLL) return fail("[%s] dimension too large.", op);
+  (void)res;
+  return 0;
+}
+
+}  // namespace
+}  // namespace iqmm
+
+using namespace iqmm;
+
+extern "C" {
+
+const char* iqmm_last_error(void) { return g_last_error.c_str(); }
+
+const char* iqmm_version(void) { return "iqmm 0.1 gfx950"; }
+
+int iqmm_quantized_matmul(iqmm_array* res, iqmm_array x, iqmm_array w, iqmm_array scales,
+                          iqmm_array biases, bool transpose, iqmm_optional_int group_size,
+                          iqmm_optional_int bits, const char* mode, iqmm_stream stream) {
+  const char* op = "quantized_matmul";
+  g_last_error.clear();
+  QParams q;
+  if (resolve(op, mode, group_size, bits, q)) return 1;
+  int64_t M, N, K;
+  int sdt;
+  if (qmm_common(op, res, x, w, scales, biases, transpose, q, M, N, K, &sdt)) return 1;
+
+  QmmArgs a{};
+  const int xb_nd = x.ndim >= 2 ? x.ndim - 2 : 0, wb_nd = w.ndim - 2;
+  std::vector<int64_t> out_shape, bshape;
+  if (wb_nd == 0) {
+    // unbatched weight: every leading dim of x folds into M
+    int64_t Mf = 1;
+    for (int i = 0; i + 1 < x.ndim; ++i) Mf *= x.shape[i];
+    for (int i = 0; i + 1 < x.ndim; ++i) out_shape.push_back(x.shape[i]);
+    out_shape.push_back(N);
+    a.M = static_cast<int>(Mf);
+    if (Mf > 0x7fffffffLL) return fail("[%s] too many rows.", op);
+    a.nbatch = 1;
+    a.bm.ndim = 0;
+  } else {
+    if (broadcast2(op, x.shape, xb_nd, w.shape, wb_nd, a.bm, bshape)) return 1;
+    out_shape = bshape;
+    if (x.ndim >= 2) out_shape.push_back(M);
+    out_shape.push_back(N);
+    a.M = static_cast<int>(M);
+    a.nbatch = 1;
+    for (auto d : bshape) a.nbatch *= d;
+  }
+  bool query;
+  if (set_or_check_res(op, res, out_shape, x.dtype, &query)) return 1;
+  if (query) return 0;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t out_n = numel(*res);
+  if (out_n == 0) return 0;
+  if (K == 0) {
+    hipError_t e = fill_zero(res->data, x.dtype, out_n, st);
+    return e == hipSuccess ? 0 : hip_fail(op, e);
+  }
+  a.x = x.data; a.w = static_cast<const uint32_t*>(w.data); a.s = scales.data; a.b = biases.data;
+  a.out = res->data;
+  a.N = static_cast<int>(N); a.K = static_cast<int>(K);
+  a.gs = q.gs; a.bits = q.bits; a.mode = q.mode; a.xdt = x.dtype; a.transpose = transpose;
+  a.x_mat = M * K;
+  a.w_mat = w.shape[w.ndim - 2] * w.shape[w.ndim - 1];
+  a.s_mat = scales.shape[scales.ndim - 2] * scales.shape[scales.ndim - 1];
+  int64_t nxm = 1, nwm = 1;
+  for (int i = 0; i < xb_nd; ++i) nxm *= x.shape[i];
+  for (int i = 0; i < wb_nd; ++i) nwm *= w.shape[i];
+  a.bm.nx = nxm; a.bm.nw = nwm; a.bm.lhs = nullptr; a.bm.rhs = nullptr;
+  a.stream = st;
+  hipError_t e = run_qmm(a);
+  return e == hipSuccess ? 0 : hip_fail(op, e);
+}
+
+int iqmm_gather_qmm(iqmm_array* res, iqmm_array x, iqmm_array w, iqmm_array scales,
+                    iqmm_array biases, iqmm_array lhs, iqmm_array rhs, bool transpose,
+                    iqmm_optional_int group_size, iqmm_optional_int bits, const char* mode,
+                    bool sorted_indices, iqmm_stream stream) {
+  const char* op = "gather_qmm";
+  g_last_error.clear();
+  (void)sorted_indices;
+  QParams q;
+  if (resolve(op, mode, group_size, bits, q)) return 1;
+  if (!present(x) || x.ndim < 2) return fail("[%s] x must have at least two dimensions.", op);
+  int64_t M, N, K;
+  int sdt;
+  if (qmm_common(op, res, x, w, scales, biases, transpose, q, M, N, K, &sdt)) return 1;
+  const int xb_nd = x.ndim - 2, wb_nd = w.ndim - 2;
+  QmmArgs a{};
+  // index arrays: absent -> arange over the operand's batch, shaped like it
+  const int64_t* lshape = present(lhs) ? lhs.shape : x.shape;
+  const int lnd = present(lhs) ? lhs.ndim : xb_nd;
+  const int64_t* rshape = present(rhs) ? rhs.shape : w.shape;
+  const int rnd = present(rhs) ? rhs.ndim : wb_nd;
+  if (present(lhs) && !is_index(lhs.dtype)) return fail("[%s] lhs_indices must be integers, got %s.", op, dt_name(lhs.dtype));
+  if (present(rhs) && !is_index(rhs.dtype)) return fail("[%s] rhs_indices must be integers, got %s.", op, dt_name(rhs.dtype));
+  std::vector<int64_t> bshape;
+  if (broadcast2(op, lshape, lnd, rshape, rnd, a.bm, bshape)) return 1;
+  std::vector<int64_t> out_shape = bshape;
+  out_shape.push_back(M);
+  out_shape.push_back(N);
+  bool query;
+  if (set_or_check_res(op, res, out_shape, x.dtype, &query)) return 1;
+  if (query) return 0;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t out_n = numel(*res);
+  if (out_n == 0) return 0;
+  if (K == 0) {
+    hipError_t e = fill_zero(res->data, x.dtype, out_n, st);
+    return e == hipSuccess ? 0 : hip_fail(op, e);
+  }
+  a.x = x.data; a.w = static_cast<const uint32_t*>(w.data); a.s = scales.data; a.b = biases.data;
+  a.out = res->data;
+  a.M = static_cast<int>(M); a.N = static_cast<int>(N); a.K = static_cast<int>(K);
+  a.gs = q.gs; a.bits = q.bits; a.mode = q.mode; a.xdt = x.dtype; a.transpose = transpose;
+  a.x_mat = M * K;
+  a.w_mat = w.shape[w.ndim - 2] * w.shape[w.ndim - 1];
+  a.s_mat = scales.shape[scales.ndim - 2] * scales.shape[scales.ndim - 1];
+  a.nbatch = 1;
+  for (auto d : bshape) a.nbatch *= d;
+  int64_t nxm = 1, nwm = 1;
+  for (int i = 0; i < xb_nd; ++i) nxm *= x.shape[i];
+  for (int i = 0; i < wb_nd; ++i) nwm *= w.shape[i];
+  a.bm.nx = nxm; a.bm.nw = nwm;
+  a.bm.lhs = present(lhs) ? lhs.data : nullptr;
+  a.bm.rhs = present(rhs) ? rhs.data : nullptr;
+  a.bm.lhs_dt = lhs.dtype; a.bm.rhs_dt = rhs.dtype;
+  a.stream = st;
+  hipError_t e = run_qmm(a);
+  return e == hipSuccess ? 0 : hip_fail(op, e);
+}
+
+int iqmm_dequantize(iqmm_array* res, iqmm_array w, iqmm_array scales, iqmm_array biases,
+                    iqmm_optional_int group_size, iqmm_optional_int bits, const char* mode,
+                    iqmm_optional_dtype dtype, iqmm_stream stream) {
+  const char* op = "dequantize";
+  g_last_error.clear();
+  QParams q;
+  if (resolve(op, mode, group_size, bits, q)) return 1;
+  if (!present(w) || w.ndim < 2) return fail("[%s] The matrix to be dequantized must have at least 2 dimensions but it has only %d.", op, w.ndim);
+  if (w.dtype != IQMM_UINT32) return fail("[%s] The matrix should be given as a uint32 but received %s.", op, dt_name(w.dtype));
+  const int64_t wlast = w.shape[w.ndim - 1];
+  if ((wlast * 32) % q.bits != 0) return fail("[%s] packed width %lld is not a whole number of %d-bit codes.", op, (long long)wlast, q.bits);
+  const int64_t K = wlast * 32 / q.bits;
+  if (K % q.gs != 0) return fail("[%s] The unpacked width %lld is not divisible by group_size %d.", op, (long long)K, q.gs);
+  int sdt;
+  if (check_scales(op, q, w, scales, biases, K / q.gs, &sdt)) return 1;
+  int odt = q.mode == AFFINE ? sdt : IQMM_BFLOAT16;
+  if (dtype.has_value) {
+    if (!is_float(dtype.value)) return fail("[%s] Output dtype must be a floating type, got %s.", op, dt_name(dtype.value));
+    odt = dtype.value;
+  }
+  std::vector<int64_t> out_shape(w.shape, w.shape + w.ndim);
+  out_shape.back() = K;
+  bool query;
+  if (set_or_check_res(op, res, out_shape, odt, &query)) return 1;
+  if (query) return 0;
+  ConvArgs a{};
+  a.w = static_cast<const uint32_t*>(w.data); a.s = scales.data; a.b = biases.data; a.out = res->data;
+  a.rows = numel(w) / (wlast > 0 ? wlast : 1);
+  if (wlast == 0) return 0;
+  if (K > 0x7fffffffLL) return fail("[%s] row too long.", op);
+  a.K = static_cast<int>(K); a.gs = q.gs; a.bits = q.bits; a.mode = q.mode; a.sdt = sdt; a.odt = odt;
+  a.stream = static_cast<hipStream_t>(stream);
+  hipError_t e = launch_dequantize(a);
+  return e == hipSuccess ? 0 : hip_fail(op, e);
+}
+
+int iqmm_quantize(iqmm_array* res_w, iqmm_array* res_scales, iqmm_array* res_biases,
+                  iqmm_array w, iqmm_optional_int group_size, iqmm_optional_int bits,
+                  const char* mode, iqmm_stream stream) {
+  const char* op = "quantize";
+  g_last_error.clear();
+  QParams q;
+  if (resolve(op, mode, group_size, bits, q)) return 1;
+  if (!present(w) || w.ndim < 2) return fail("[%s] The matrix to be quantized must have at least 2 dimensions but it has only %d.", op, w.ndim);
+  if (!is_float(w.dtype)) return fail("[%s] Only real floating types can be quantized but w has type %s.", op, dt_name(w.dtype));
+  const int64_t K = w.shape[w.ndim - 1];
+  if (K % q.gs != 0)
+    return fail("[%s] The last dimension of the matrix needs to be divisible by the quantization group size %d. However the provided matrix has shape %s", op, q.gs, shape_str(w).c_str());
+  if ((K * q.bits) % 32 != 0) return fail("[%s] K*bits must be a multiple of 32.", op);
+  std::vector<int64_t> wq_shape(w.shape, w.shape + w.ndim), s_shape(w.shape, w.shape + w.ndim);
+  wq_shape.back() = K * q.bits / 32;
+  s_shape.back() = K / q.gs;
+  const int sdt = q.mode == AFFINE ? w.dtype : IQMM_UINT8;
+  bool q1, q2, q3 = true;
+  if (set_or_check_res(op, res_w, wq_shape, IQMM_UINT32, &q1)) return 1;
+  if (set_or_check_res(op, res_scales, s_shape, sdt, &q2)) return 1;
+  if (q.mode == AFFINE) {
+    if (set_or_check_res(op, res_biases, s_shape, sdt, &q3)) return 1;
+  } else if (res_biases) {
+    res_biases->ndim = 0;
+    res_biases->data = nullptr;
+  }
+  if (q1 || q2 || (q.mode == AFFINE && q3)) {
+    if (!(q1 && q2 && (q.mode != AFFINE || q3)))
+      return fail("[%s] either all result buffers are allocated or none.", op);
+    return 0;
+  }
+  ConvArgs a{};
+  a.src = w.data; a.wq = static_cast<uint32_t*>(res_w->data); a.sq = res_scales->data;
+  a.bq = q.mode == AFFINE ? res_biases->data : nullptr;
+  a.rows = K > 0 ? numel(w) / K : 0;
+  if (K > 0x7fffffffLL) return fail("[%s] row too long.", op);
+  a.K = static_cast<int>(K); a.gs = q.gs; a.bits = q.bits; a.mode = q.mode; a.sdt = w.dtype;
+  a.stream = static_cast<hipStream_t>(stream);
+  hipError_t e = launch_quantize(a);
+  return e == hipSuccess ? 0 : hip_fail(op, e);
+}
+
+}  // extern "C"

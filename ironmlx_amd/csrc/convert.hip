@@ -1,0 +1,271 @@
+// convert.hip — dequantize and quantize on the GPU.
+//
+// dequantize (mlx/src/ops.rs:653-686; caller mlx/src/nn/embedding.rs:62-72):
+//   one thread per 32-code chunk: `bits` words in, 32 values out, bit-exact:
+//   affine  v = rn(rn(s * q) + b)  (multiply and add rounded separately),
+//   fp      v = rn(elem(q) * scale), then RNE to the output dtype.
+// quantize (mlx_quantize; makes the packed inputs):
+//   one thread per quantization group, same arithmetic as MLX's per-group
+//   rule (see oracle/iqmm_oracle.c for the restated rule), so codes, scales
+//   and biases are bit-identical to the CPU restatement.  Divisions are IEEE
+//   correctly rounded (hipcc's default for fp32 '/').
+#include "launch.h"
+
+namespace iqmm {
+
+#pragma clang fp contract(off)
+
+template <int SDT, int ODT, int MODE, int BITS>
+__global__ __launch_bounds__(256) void dequant_kernel(ConvArgs a, int64_t nchunks) {
+  const int64_t id = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (id >= nchunks) return;
+  using OS = typename Store<ODT>::T;
+  constexpr bool AFF = MODE == AFFINE;
+  const int K = a.K;
+  const int cpr = (K + 31) >> 5;                 // chunks per row
+  const int64_t row = id / cpr;
+  const int c = static_cast<int>(id - row * cpr);
+  const int k0 = c * 32;
+  const int ncode = min(32, K - k0);
+  const int64_t wpr = static_cast<int64_t>(K) * BITS / 32;
+  const uint32_t* src = a.w + row * wpr + static_cast<int64_t>(c) * BITS;
+  uint32_t wd[BITS];
+  if (ncode == 32) {
+    load_chunk<BITS>(wd, src);
+  } else {
+    const int nw = (ncode * BITS + 31) / 32;
+#pragma unroll
+    for (int i = 0; i < BITS; ++i) wd[i] = i < nw ? src[i] : 0u;
+  }
+  const int gs = AFF ? a.gs : ModeInfo<MODE>::GS;
+  const int G = K / gs;
+  OS vals[32];
+#pragma unroll
+  for (int j = 0; j < 32; ++j) {
+    const int k = k0 + j;
+    const int64_t gi = row * G + (k < K ? k : K - 1) / gs;
+    const uint32_t q = chunk_code<BITS>(wd, j);
+    float v;
+    if constexpr (AFF) {
+      using SS = typename Store<SDT>::T;
+      const float s = to_f<SDT>(static_cast<const SS*>(a.s)[gi]);
+      const float b = to_f<SDT>(static_cast<const SS*>(a.b)[gi]);
+      const float p = s * static_cast<float>(q);
+      v = p + b;
+    } else {
+      v = fp_elem<MODE>(q) * fp_scale<MODE>(static_cast<const uint8_t*>(a.s)[gi]);
+    }
+    vals[j] = from_f<ODT>(v);
+  }
+  OS* dst = static_cast<OS*>(a.out) + row * K + k0;
+  if (ncode == 32 && sizeof(OS) == 2) {
+    uint4* d4 = reinterpret_cast<uint4*>(dst);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t u[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        u[j] = static_cast<uint32_t>(vals[8 * i + 2 * j]) |
+               (static_cast<uint32_t>(vals[8 * i + 2 * j + 1]) << 16);
+      d4[i] = make_uint4(u[0], u[1], u[2], u[3]);
+    }
+  } else {
+    for (int j = 0; j < ncode; ++j) dst[j] = vals[j];
+  }
+}
+
+// round-to-nearest-even onto the element grid with saturation, written as the
+// same grid search as the CPU restatement so ties and zero signs agree
+template <int MODE>
+__device__ __forceinline__ uint32_t nearest_code(float v) {
+  constexpr int NPOS = MODE == MXFP8 ? 127 : 8;
+  constexpr uint32_t SIGN = MODE == MXFP8 ? 0x80u : 0x8u;
+  const float top = fp_elem<MODE>(NPOS - 1);
+  float av = fminf(fabsf(v), top);
+  if (__builtin_isnan(v)) return 0u;
+  uint32_t best = 0;
+  float gb = 0.f;
+  for (int c = 1; c < NPOS; ++c) {
+    const float g = fp_elem<MODE>(static_cast<uint32_t>(c));
+    const float dg = fabsf(av - g), db = fabsf(av - gb);
+    if (dg < db || (dg == db && (c & 1) == 0 && (best & 1u) == 1u)) {
+      best = static_cast<uint32_t>(c);
+      gb = g;
+    }
+  }
+  const bool neg = v < 0.f || (v == 0.f && __builtin_signbit(v));
+  return (neg && best != 0u) ? (best | SIGN) : best;
+}
+
+template <int WDT, int MODE, int BITS>
+__global__ __launch_bounds__(256) void quant_kernel(ConvArgs a, int64_t ngroups) {
+  const int64_t id = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (id >= ngroups) return;
+  using WS = typename Store<WDT>::T;
+  const int K = a.K;
+  constexpr bool AFF = MODE == AFFINE;
+  const int gs = AFF ? a.gs : ModeInfo<MODE>::GS;
+  const int G = K / gs;
+  const int64_t row = id / G;
+  const int g = static_cast<int>(id - row * G);
+  const WS* src = static_cast<const WS*>(a.src) + row * K + static_cast<int64_t>(g) * gs;
+  const int64_t wpr = static_cast<int64_t>(K) * BITS / 32;
+  // a group of gs codes fills gs*BITS/32 whole words (gs*BITS is a multiple of 32)
+  uint32_t* dstw = a.wq + row * wpr + static_cast<int64_t>(g) * gs * BITS / 32;
+  const int nwords = gs * BITS / 32;
+
+  if constexpr (AFF) {
+    const float n_bins = static_cast<float>((1 << BITS) - 1), eps = 1e-7f;
+    float wmax = -__builtin_inff(), wmin = __builtin_inff();
+    for (int j = 0; j < gs; ++j) {
+      const float v = to_f<WDT>(src[j]);
+      wmax = fmaxf(wmax, v);
+      wmin = fminf(wmin, v);
+    }
+    const bool mask = fabsf(wmin) > fabsf(wmax);
+    float scale = fmaxf((wmax - wmin) / n_bins, eps);
+    scale = mask ? scale : -scale;
+    const float edge = mask ? wmin : wmax;
+    const float q0 = rintf(edge / scale);
+    float bias = 0.f;
+    if (q0 != 0.f) {
+      scale = edge / q0;
+      bias = edge;
+    }
+    for (int wi = 0; wi < nwords; ++wi) {
+      // codes overlapping word wi: bits [32wi, 32wi+32)
+      uint32_t word = 0;
+      const int jlo = (32 * wi) / BITS, jhi = min(gs - 1, (32 * wi + 31) / BITS);
+      for (int j = jlo; j <= jhi; ++j) {
+        float q = rintf((to_f<WDT>(src[j]) - bias) / scale);
+        q = fminf(fmaxf(q, 0.f), n_bins);
+        const uint32_t qi = static_cast<uint32_t>(q);
+        const int bit = j * BITS - 32 * wi;
+        word |= bit >= 0 ? (qi << bit) : (qi >> (-bit));
+      }
+      dstw[wi] = word;
+    }
+    using SS = typename Store<WDT>::T;
+    static_cast<SS*>(a.sq)[id] = from_f<WDT>(scale);
+    static_cast<SS*>(a.bq)[id] = from_f<WDT>(bias);
+  } else {
+    float amax = 0.f;
+    for (int j = 0; j < gs; ++j) amax = fmaxf(amax, fabsf(to_f<WDT>(src[j])));
+    uint32_t sc;
+    float sdec;
+    if constexpr (MODE == NVFP4) {
+      sc = nearest_code<MXFP8>(amax / 6.0f);   // e4m3 block scale
+      sdec = e4m3_to_f(sc);
+    } else {
+      constexpr int emax_elem = MODE == MXFP8 ? 8 : 2;
+      int ex = 0;
+      if (amax > 0.f) frexpf(amax, &ex);
+      int e = amax > 0.f ? (ex - 1) - emax_elem : -127;
+      e = e < -127 ? -127 : (e > 127 ? 127 : e);
+      sc = static_cast<uint32_t>(e + 127);
+      sdec = ldexpf(1.0f, e);
+    }
+    for (int wi = 0; wi < nwords; ++wi) {
+      uint32_t word = 0;
+      const int per = 32 / BITS;
+      for (int j = 0; j < per; ++j) {
+        const float v = sdec > 0.f ? to_f<WDT>(src[wi * per + j]) / sdec : 0.f;
+        word |= nearest_code<MODE>(v) << (j * BITS);
+      }
+      dstw[wi] = word;
+    }
+    static_cast<uint8_t*>(a.sq)[id] = static_cast<uint8_t>(sc);
+  }
+}
+
+namespace {
+template <int SDT, int ODT>
+hipError_t deq_by_mode(const ConvArgs& a, int64_t nchunks, dim3 grid) {
+#define IQMM_D(MODE, BITS) \
+  hipLaunchKernelGGL((dequant_kernel<SDT, ODT, MODE, BITS>), grid, dim3(256), 0, a.stream, a, nchunks); \
+  return hipGetLastError()
+  switch (a.mode) {
+    case AFFINE:
+      switch (a.bits) {
+        case 2: IQMM_D(AFFINE, 2);
+        case 3: IQMM_D(AFFINE, 3);
+        case 4: IQMM_D(AFFINE, 4);
+        case 5: IQMM_D(AFFINE, 5);
+        case 6: IQMM_D(AFFINE, 6);
+        case 8: IQMM_D(AFFINE, 8);
+      }
+      break;
+    case MXFP4: IQMM_D(MXFP4, 4);
+    case MXFP8: IQMM_D(MXFP8, 8);
+    case NVFP4: IQMM_D(NVFP4, 4);
+  }
+#undef IQMM_D
+  return hipErrorInvalidValue;
+}
+
+template <int ODT>
+hipError_t deq_by_sdt(const ConvArgs& a, int64_t nchunks, dim3 grid) {
+  if (a.mode != AFFINE) return deq_by_mode<U8, ODT>(a, nchunks, grid);
+  switch (a.sdt) {
+    case F32: return deq_by_mode<F32, ODT>(a, nchunks, grid);
+    case F16: return deq_by_mode<F16, ODT>(a, nchunks, grid);
+    case BF16: return deq_by_mode<BF16, ODT>(a, nchunks, grid);
+  }
+  return hipErrorInvalidValue;
+}
+
+template <int WDT>
+hipError_t quant_by_mode(const ConvArgs& a, int64_t ngroups, dim3 grid) {
+#define IQMM_Q(MODE, BITS) \
+  hipLaunchKernelGGL((quant_kernel<WDT, MODE, BITS>), grid, dim3(256), 0, a.stream, a, ngroups); \
+  return hipGetLastError()
+  switch (a.mode) {
+    case AFFINE:
+      switch (a.bits) {
+        case 2: IQMM_Q(AFFINE, 2);
+        case 3: IQMM_Q(AFFINE, 3);
+        case 4: IQMM_Q(AFFINE, 4);
+        case 5: IQMM_Q(AFFINE, 5);
+        case 6: IQMM_Q(AFFINE, 6);
+        case 8: IQMM_Q(AFFINE, 8);
+      }
+      break;
+    case MXFP4: IQMM_Q(MXFP4, 4);
+    case MXFP8: IQMM_Q(MXFP8, 8);
+    case NVFP4: IQMM_Q(NVFP4, 4);
+  }
+#undef IQMM_Q
+  return hipErrorInvalidValue;
+}
+}  // namespace
+
+hipError_t launch_dequantize(const ConvArgs& a) {
+  const int64_t nchunks = a.rows * ((a.K + 31) / 32);
+  if (nchunks == 0) return hipSuccess;
+  const int64_t nblk = (nchunks + 255) / 256;
+  if (nblk > 0x7fffffffLL) return hipErrorInvalidConfiguration;
+  dim3 grid(static_cast<unsigned>(nblk));
+  switch (a.odt) {
+    case F32: return deq_by_sdt<F32>(a, nchunks, grid);
+    case F16: return deq_by_sdt<F16>(a, nchunks, grid);
+    case BF16: return deq_by_sdt<BF16>(a, nchunks, grid);
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_quantize(const ConvArgs& a) {
+  const int gs = a.gs;
+  const int64_t ngroups = a.rows * (a.K / gs);
+  if (ngroups == 0) return hipSuccess;
+  const int64_t nblk = (ngroups + 255) / 256;
+  if (nblk > 0x7fffffffLL) return hipErrorInvalidConfiguration;
+  dim3 grid(static_cast<unsigned>(nblk));
+  switch (a.sdt) {  // sdt carries the source (w) dtype for quantize
+    case F32: return quant_by_mode<F32>(a, ngroups, grid);
+    case F16: return quant_by_mode<F16>(a, ngroups, grid);
+    case BF16: return quant_by_mode<BF16>(a, ngroups, grid);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace iqmm

@@ -1,0 +1,51 @@
+// launch.h — host-side launch interface between the C-ABI dispatcher
+// (api.hip) and the kernel translation units.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "common.h"
+
+namespace iqmm {
+
+// One quantized-matmul problem: out[b] = x[xb(b)] (M x K) . W[wb(b)]^T (or W).
+struct QmmArgs {
+  const void* x;
+  const uint32_t* w;
+  const void* s;
+  const void* b;  // biases (affine) or nullptr
+  void* out;
+  int M, N, K;
+  int gs, bits, mode, xdt;
+  bool transpose;
+  int64_t x_mat;  // elements per x matrix (M*K)
+  int64_t w_mat;  // uint32 words per w matrix
+  int64_t s_mat;  // scale entries per w matrix
+  int64_t nbatch;
+  BatchMap bm;
+  hipStream_t stream;
+};
+
+// Dequantize / quantize problems over `rows` rows of K values.
+struct ConvArgs {
+  const uint32_t* w;  // packed (dequantize input)
+  const void* s;
+  const void* b;
+  void* out;          // dequantize output
+  const void* src;    // quantize input
+  uint32_t* wq;       // quantize outputs
+  void* sq;
+  void* bq;
+  int64_t rows;
+  int K, gs, bits, mode, sdt, odt;
+  hipStream_t stream;
+};
+
+hipError_t launch_qmv(const QmmArgs& a);        // transpose=true, small M, VALU
+hipError_t launch_qvm(const QmmArgs& a);        // transpose=false, small M, VALU
+hipError_t launch_qmm_mfma(const QmmArgs& a);   // bf16/fp16 MFMA tiles, any M
+bool qmm_mfma_supported(const QmmArgs& a);
+hipError_t launch_dequantize(const ConvArgs& a);
+hipError_t launch_quantize(const ConvArgs& a);
+
+}  // namespace iqmm

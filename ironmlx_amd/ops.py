@@ -1,0 +1,164 @@
+"""Host-side mirror of ironmlx's quantized ops over the C ABI.
+
+Same names, argument order, argument meaning, defaults and error behaviour as
+the Rust wrappers in ``mlx/src/ops.rs``:
+
+* ``dequantize(w, scales, biases, group_size, bits, mode, stream)``
+  -- ``mlx/src/ops.rs:653-686``
+* ``quantized_matmul(x, w, scales, biases, transpose, group_size, bits, mode,
+  stream)`` -- ``mlx/src/ops.rs:695-727``
+* ``gather_qmm(...)`` -- mlx-c's ``mlx_gather_qmm`` (ironmlx has no wrapper;
+  its MoE loop ``mlx/src/nn/moe.rs:84-170`` is what it replaces)
+* ``quantize(w, group_size, bits, mode)`` -- mlx-c's ``mlx_quantize``
+
+Arrays are torch tensors on a ROCm device (torch only provides device memory
+and the stream); every computation runs in the HIP library libiqmm.so.
+Failures raise :class:`IqmmError` with the library's message, as the Rust
+wrappers return ``Err(Error::Mlx(msg))``.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Sequence, Tuple
+
+import torch
+
+from . import _lib
+from ._lib import IqmmError
+
+_TORCH_TO_DT = {
+    torch.float32: _lib.FLOAT32, torch.float16: _lib.FLOAT16, torch.bfloat16: _lib.BFLOAT16,
+    torch.uint32: _lib.UINT32, torch.int32: _lib.INT32, torch.uint8: _lib.UINT8,
+    torch.int64: _lib.INT64,
+}
+_DT_TO_TORCH = {_lib.FLOAT32: torch.float32, _lib.FLOAT16: torch.float16,
+                _lib.BFLOAT16: torch.bfloat16, _lib.UINT32: torch.uint32,
+                _lib.UINT8: torch.uint8, _lib.INT32: torch.int32, _lib.INT64: torch.int64}
+
+
+def _device_of(*ts) -> torch.device:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise IqmmError("iqmm ops run on the GPU only; got a tensor on "
+                            f"{t.device} (there is no CPU path)")
+        if dev is not None and t.device != dev:
+            raise IqmmError(f"tensors on different devices: {dev} and {t.device}")
+        dev = t.device
+    return dev
+
+
+def _arr(t: Optional[torch.Tensor], packed: bool = False) -> _lib.IqmmArray:
+    a = _lib.IqmmArray()
+    if t is None:
+        return a
+    if not t.is_contiguous():
+        raise IqmmError("iqmm ops take C-contiguous arrays")
+    if t.dim() > _lib.MAX_NDIM:
+        raise IqmmError(f"too many dimensions ({t.dim()})")
+    a.data = t.data_ptr() if t.numel() > 0 else (t.data_ptr() or 1)
+    for i, s in enumerate(t.shape):
+        a.shape[i] = s
+    a.ndim = t.dim()
+    dt = _TORCH_TO_DT.get(t.dtype)
+    if dt is None:
+        raise IqmmError(f"unsupported dtype {t.dtype}")
+    # packed weights may arrive as int32 views of the uint32 words
+    a.dtype = _lib.UINT32 if (packed and dt == _lib.INT32) else dt
+    return a
+
+
+def _stream(dev: torch.device, stream) -> ctypes.c_void_p:
+    if stream is None:
+        stream = torch.cuda.current_stream(dev)
+    return ctypes.c_void_p(stream.cuda_stream)
+
+
+def _alloc(res: _lib.IqmmArray, dev) -> torch.Tensor:
+    shape = tuple(res.shape[i] for i in range(res.ndim))
+    dt = _DT_TO_TORCH[res.dtype]
+    if dt == torch.uint32:
+        return torch.empty(shape, dtype=torch.int32, device=dev).view(torch.uint32)
+    return torch.empty(shape, dtype=dt, device=dev)
+
+
+def _run(fn, res: _lib.IqmmArray, dev, args) -> torch.Tensor:
+    _lib.check(fn(ctypes.byref(res), *args))          # shape/dtype inference
+    out = _alloc(res, dev)
+    res.data = out.data_ptr() if out.numel() > 0 else 1
+    _lib.check(fn(ctypes.byref(res), *args))
+    return out
+
+
+def _mode(mode: str) -> bytes:
+    return (mode or "affine").encode()
+
+
+def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
+                     biases: Optional[torch.Tensor] = None, transpose: bool = True,
+                     group_size: Optional[int] = None, bits: Optional[int] = None,
+                     mode: str = "affine", stream=None) -> torch.Tensor:
+    """``x @ dequantize(w, scales, biases)^T`` (``transpose``) or ``x @
+    dequantize(w)``; mirrors ``ops::quantized_matmul`` (mlx/src/ops.rs:695-727)."""
+    L = _lib.load()
+    dev = _device_of(x, w, scales, biases)
+    args = (_arr(x), _arr(w, True), _arr(scales), _arr(biases), bool(transpose),
+            _lib.opt_int(group_size), _lib.opt_int(bits), _mode(mode), _stream(dev, stream))
+    return _run(L.iqmm_quantized_matmul, _lib.IqmmArray(), dev, args)
+
+
+def dequantize(w: torch.Tensor, scales: torch.Tensor, biases: Optional[torch.Tensor] = None,
+               group_size: Optional[int] = None, bits: Optional[int] = None,
+               mode: str = "affine", stream=None,
+               dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """Unpack and rescale; mirrors ``ops::dequantize`` (mlx/src/ops.rs:653-686).
+    ``dtype`` is mlx-c's optional output dtype (ironmlx always passes none)."""
+    L = _lib.load()
+    dev = _device_of(w, scales, biases)
+    od = _lib.OptionalDtype(0, False) if dtype is None else \
+        _lib.OptionalDtype(_TORCH_TO_DT[dtype], True)
+    args = (_arr(w, True), _arr(scales), _arr(biases), _lib.opt_int(group_size),
+            _lib.opt_int(bits), _mode(mode), od, _stream(dev, stream))
+    return _run(L.iqmm_dequantize, _lib.IqmmArray(), dev, args)
+
+
+def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
+               biases: Optional[torch.Tensor] = None,
+               lhs_indices: Optional[torch.Tensor] = None,
+               rhs_indices: Optional[torch.Tensor] = None, transpose: bool = True,
+               group_size: Optional[int] = None, bits: Optional[int] = None,
+               mode: str = "affine", sorted_indices: bool = False, stream=None) -> torch.Tensor:
+    """``out[i] = x[lhs[i]] @ dequantize(w[rhs[i]])^T`` over the broadcast index
+    shape; mirrors mlx-c ``mlx_gather_qmm``."""
+    L = _lib.load()
+    dev = _device_of(x, w, scales, biases, lhs_indices, rhs_indices)
+    args = (_arr(x), _arr(w, True), _arr(scales), _arr(biases), _arr(lhs_indices),
+            _arr(rhs_indices), bool(transpose), _lib.opt_int(group_size), _lib.opt_int(bits),
+            _mode(mode), bool(sorted_indices), _stream(dev, stream))
+    return _run(L.iqmm_gather_qmm, _lib.IqmmArray(), dev, args)
+
+
+def quantize(w: torch.Tensor, group_size: Optional[int] = None, bits: Optional[int] = None,
+             mode: str = "affine", stream=None
+             ) -> Tuple[torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
+    """Quantize along the last axis; returns (w_q uint32, scales, biases|None);
+    mirrors mlx-c ``mlx_quantize``."""
+    L = _lib.load()
+    dev = _device_of(w)
+    rw, rs, rb = _lib.IqmmArray(), _lib.IqmmArray(), _lib.IqmmArray()
+    args = (_arr(w), _lib.opt_int(group_size), _lib.opt_int(bits), _mode(mode),
+            _stream(dev, stream))
+    _lib.check(L.iqmm_quantize(ctypes.byref(rw), ctypes.byref(rs), ctypes.byref(rb), *args))
+    tw, ts = _alloc(rw, dev), _alloc(rs, dev)
+    tb = _alloc(rb, dev) if rb.ndim > 0 else None
+    rw.data, rs.data = tw.data_ptr() or 1, ts.data_ptr() or 1
+    if tb is not None:
+        rb.data = tb.data_ptr() or 1
+    _lib.check(L.iqmm_quantize(ctypes.byref(rw), ctypes.byref(rs),
+                               ctypes.byref(rb) if tb is not None else None, *args))
+    return tw, ts, tb
+
+
+__all__ = ["quantized_matmul", "dequantize", "gather_qmm", "quantize", "IqmmError"]

@@ -20,10 +20,13 @@ Parity status of each function (how it is pinned, see tests/test_oracle.py):
   * qmm / qmv: pinned by float64 numpy matmul of the dequantized weight and
     by special cases (one-hot x selects a row, bits=8 s=1 b=0 is an integer
     GEMM, constant scale factors out).
-  * affine_quantize / fp_quantize: pinned by invariants only (code range,
-    reconstruction error <= |scale|/2, exact group edge, idempotence of
-    quantize(dequantize(.))).  MLX's own tie/eps/scale-selection choices are
-    unverifiable here: "parity unpinned" against MLX itself.
+  * affine_quantize: pinned by a hand-derived known answer (sign/edge-snap
+    rule) and invariants (code range, reconstruction error <= |scale|/2 for
+    interior codes, exact larger-magnitude group edge).
+  * fp_quantize: pinned by invariants (OCP shared-exponent rule, nvfp4
+    block scale = RNE(amax/6), each element the nearest grid point by brute
+    force).  MLX's own tie/eps/scale-selection choices for quantize are not
+    verifiable without MLX: "parity unpinned" against MLX itself.
 """
 from __future__ import annotations
 
@@ -80,6 +83,8 @@ def lib():
                                      i32, i32]
         L.iqo_affine_quantize.argtypes = [vp, i32, i64, i64, i32, i32, vp, vp, vp, i32]
         L.iqo_fp_quantize.argtypes = [vp, i32, i64, i64, i32, vp, vp]
+        L.iqo_from_float_array.argtypes = [vp, i64, i32, vp]
+        L.iqo_to_float_array.argtypes = [vp, i64, i32, vp]
         _lib = L
     return _lib
 
@@ -95,20 +100,22 @@ def _c(a, dtype):
 
 # ----------------------------------------------------------------- conversions
 def to_float(a: np.ndarray, dt: str) -> np.ndarray:
-    """Decode a tagged float array to float32 (element-wise via the oracle)."""
+    """Decode a tagged float array to float32 (via the oracle's decoder)."""
     if dt == "f32":
-        return a.astype(np.float32)
-    f = lib().iqo_bf16_to_float if dt == "bf16" else lib().iqo_half_to_float
-    bits = a.view(np.uint16) if dt == "f16" else a
-    return np.array([f(int(v)) for v in bits.reshape(-1)], np.float32).reshape(a.shape)
+        return np.asarray(a, np.float32)
+    src = np.ascontiguousarray(a).view(np.uint16)
+    out = np.empty(src.shape, np.float32)
+    lib().iqo_to_float_array(_p(src), src.size, DT[dt], _p(out))
+    return out
 
 
 def from_float(a: np.ndarray, dt: str) -> np.ndarray:
+    """Round float32 values to a tagged float array (RNE, via the oracle)."""
+    src = np.ascontiguousarray(a, np.float32)
     if dt == "f32":
-        return a.astype(np.float32)
-    f = lib().iqo_float_to_bf16 if dt == "bf16" else lib().iqo_float_to_half
-    out = np.array([f(float(v)) for v in np.asarray(a, np.float32).reshape(-1)], np.uint16)
-    out = out.reshape(np.shape(a))
+        return src.copy()
+    out = np.empty(src.shape, np.uint16)
+    lib().iqo_from_float_array(_p(src), src.size, DT[dt], _p(out))
     return out.view(np.float16) if dt == "f16" else out
 
 

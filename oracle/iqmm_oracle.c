@@ -380,3 +380,11 @@ int iqo_fp_quantize(const void* w, int wdt, int64_t rows, int64_t K, int mode, u
   }
   return 0;
 }
+
+/* array conversions (used by the Python wrapper for speed) */
+void iqo_from_float_array(const float* in, int64_t n, int dt, void* out) {
+  for (int64_t i = 0; i < n; ++i) store_f(out, dt, i, in[i]);
+}
+void iqo_to_float_array(const void* in, int64_t n, int dt, float* out) {
+  for (int64_t i = 0; i < n; ++i) out[i] = load_f(in, dt, i);
+}

@@ -1,0 +1,283 @@
+"""GPU parity: the HIP library (through the C ABI, via ironmlx_amd.ops) against
+the CPU oracle on identical seeded inputs.
+
+Bars: dequantize and quantize are bit-exact; matmul outputs are within
+max|got-ref| / max|ref| <= 1e-2 for bf16/fp16 outputs (fp32 accumulation) and
+<= 2e-2 for the fp8/fp4 modes; fp32 outputs within 1e-4.
+Reference surface: mlx/src/ops.rs:653-727, mlx/src/nn/moe.rs:55-183.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from helpers import (TDT, as_f64, from_np, rand_affine, rand_fp, rel_err, to_np,
+                     words_to_np, words_to_torch)
+
+pytestmark = pytest.mark.gpu
+
+TOL = {"bf16": 1e-2, "f16": 1e-2, "f32": 1e-4}
+TOL_FP = {"bf16": 2e-2, "f16": 2e-2, "f32": 1e-4}
+
+
+@pytest.fixture(scope="module")
+def ops():
+    assert torch.cuda.is_available(), "GPU tests need a ROCm device"
+    from ironmlx_amd import ops as _ops
+    from ironmlx_amd import _lib
+    _lib.load()
+    return _ops
+
+
+def _bits_equal(got: torch.Tensor, ref: np.ndarray, dt: str):
+    g = to_np(got, dt)
+    gb = g.view(np.uint32 if dt == "f32" else np.uint16)
+    rb = np.ascontiguousarray(ref).view(np.uint32 if dt == "f32" else np.uint16)
+    assert gb.shape == rb.shape
+    bad = np.nonzero(gb != rb)
+    assert bad[0].size == 0, f"{bad[0].size} mismatches, first at {[b[0] for b in bad]}: " \
+                             f"{gb[tuple(b[0] for b in bad)]:#x} vs {rb[tuple(b[0] for b in bad)]:#x}"
+
+
+# ------------------------------------------------------------------ dequantize
+@pytest.mark.parametrize("sdt", ["f16", "bf16", "f32"])
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+def test_dequantize_affine_bit_exact(ops, bits, gs, sdt):
+    rng = np.random.default_rng(100 + bits * 10 + gs)
+    w, s, b = rand_affine(rng, 37, 512, gs, bits, sdt)
+    got = ops.dequantize(words_to_torch(w), from_np(s, sdt), from_np(b, sdt), gs, bits)
+    ref = oracle.dequantize(w, s, b, sdt, gs, bits)
+    _bits_equal(got, ref, sdt)
+
+
+@pytest.mark.parametrize("odt", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("mode", ["mxfp4", "mxfp8", "nvfp4"])
+def test_dequantize_fp_bit_exact(ops, mode, odt):
+    rng = np.random.default_rng(7)
+    w, sc = rand_fp(rng, 33, 512, mode)
+    # include every element code and a spread of scale codes
+    got = ops.dequantize(words_to_torch(w), torch.from_numpy(sc).cuda(), None, mode=mode,
+                         dtype=TDT[odt])
+    ref = oracle.dequantize(w, sc, None, None, None, None, mode, odt=odt)
+    _bits_equal(got, ref, odt)
+
+
+def test_dequantize_special_values(ops):
+    # exhaustive codes x special scale/bias bit patterns (zeros, subnormals, max)
+    codes = np.tile(np.arange(256, dtype=np.uint32), (12, 1))
+    w = oracle.pack(codes, 8)
+    sbits = np.array([0x0000, 0x8000, 0x0001, 0x03FF, 0x0400, 0x7BFF, 0x3C00, 0xBC00,
+                      0x1400, 0x2E66, 0x5640, 0x0200], np.uint16)
+    s = np.repeat(sbits[:, None], 2, axis=1).view(np.float16)
+    b = np.repeat(sbits[::-1, None], 2, axis=1).view(np.float16)
+    got = ops.dequantize(words_to_torch(w), from_np(s, "f16"), from_np(b, "f16"), 128, 8)
+    ref = oracle.dequantize(w, s, b, "f16", 128, 8)
+    _bits_equal(got, ref, "f16")
+    # every e8m0 scale code (mxfp8), except NaN=255
+    codes = np.tile(np.arange(0, 127, dtype=np.uint32), (255, 1))[:, :96]
+    w = oracle.pack(codes, 8)
+    sc = np.repeat(np.arange(255, dtype=np.uint8)[:, None], 3, axis=1)
+    got = ops.dequantize(words_to_torch(w), torch.from_numpy(sc).cuda(), None, mode="mxfp8",
+                         dtype=torch.float32)
+    ref = oracle.dequantize(w, sc, None, None, None, None, "mxfp8", odt="f32")
+    _bits_equal(got, ref, "f32")
+
+
+# ------------------------------------------------------------------ quantize
+@pytest.mark.parametrize("wdt", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("bits,gs", [(2, 32), (3, 64), (4, 64), (4, 128), (5, 32), (6, 64),
+                                     (8, 128)])
+def test_quantize_affine_bit_exact(ops, bits, gs, wdt):
+    rng = np.random.default_rng(bits * 1000 + gs)
+    wf = (rng.standard_normal((40, 512)) * 0.02).astype(np.float32)
+    wf[3, :gs] = 0.0                                  # constant group -> eps scale
+    wf[5, :gs] = np.linspace(-1, 2, gs)               # q0 edge snap case
+    wn = oracle.from_float(wf, wdt)
+    tq, ts, tb = ops.quantize(from_np(wn, wdt), gs, bits)
+    rq, rs, rb = oracle.affine_quantize(wn, wdt, gs, bits)
+    assert np.array_equal(words_to_np(tq), rq)
+    _bits_equal(ts, rs, wdt)
+    _bits_equal(tb, rb, wdt)
+
+
+@pytest.mark.parametrize("wdt", ["f32", "bf16"])
+@pytest.mark.parametrize("mode", ["mxfp4", "mxfp8", "nvfp4"])
+def test_quantize_fp_bit_exact(ops, mode, wdt):
+    rng = np.random.default_rng(3)
+    wf = (rng.standard_normal((24, 512)) * 0.02).astype(np.float32)
+    wf[1, :32] = 0.0
+    wf[2, :32] *= 1e6
+    wn = oracle.from_float(wf, wdt)
+    tq, ts, tb = ops.quantize(from_np(wn, wdt), mode=mode)
+    rq, rs = oracle.fp_quantize(wn, wdt, mode)
+    assert tb is None
+    assert np.array_equal(words_to_np(tq), rq)
+    assert np.array_equal(ts.cpu().numpy(), rs)
+
+
+# ------------------------------------------------------------------ quantized_matmul
+def _qmm_case(ops, rng, M, N, K, xdt, mode="affine", bits=4, gs=64, transpose=True):
+    rows, cols = (N, K) if transpose else (K, N)
+    sdt = xdt
+    if mode == "affine":
+        w, s, b = rand_affine(rng, rows, cols, gs, bits, sdt)
+        ts, tb = from_np(s, sdt), from_np(b, sdt)
+    else:
+        w, s = rand_fp(rng, rows, cols, mode)
+        b, sdt = None, None
+        ts, tb = torch.from_numpy(s).cuda(), None
+    x = oracle.from_float(rng.standard_normal((M, K)).astype(np.float32), xdt)
+    got = ops.quantized_matmul(from_np(x, xdt), words_to_torch(w), ts, tb, transpose,
+                               None if mode != "affine" else gs,
+                               None if mode != "affine" else bits, mode)
+    ref = oracle.qmm(x, xdt, w, s, b, sdt or "f32", transpose, gs if mode == "affine" else None,
+                     bits if mode == "affine" else None, mode, odt="f32")
+    assert tuple(got.shape) == (M, N) and got.dtype == TDT[xdt]
+    return as_f64(to_np(got, xdt), xdt), ref.astype(np.float64)
+
+
+@pytest.mark.parametrize("xdt", ["f16", "bf16", "f32"])
+@pytest.mark.parametrize("M", [1, 3, 8, 17, 130])
+def test_qmm_affine4_gs64(ops, M, xdt):
+    rng = np.random.default_rng(M)
+    got, ref = _qmm_case(ops, rng, M, 320, 1024, xdt)
+    assert rel_err(got, ref) <= TOL[xdt]
+
+
+@pytest.mark.parametrize("M", [1, 5, 64])
+@pytest.mark.parametrize("bits", [2, 3, 5, 6, 8])
+@pytest.mark.parametrize("gs", [32, 128])
+def test_qmm_affine_bits(ops, bits, gs, M):
+    rng = np.random.default_rng(bits * 7 + gs + M)
+    got, ref = _qmm_case(ops, rng, M, 192, 512, "bf16", bits=bits, gs=gs)
+    assert rel_err(got, ref) <= TOL["bf16"]
+
+
+@pytest.mark.parametrize("xdt", ["bf16", "f16"])
+@pytest.mark.parametrize("M", [1, 4, 40])
+@pytest.mark.parametrize("mode", ["mxfp4", "mxfp8", "nvfp4"])
+def test_qmm_fp_modes(ops, mode, M, xdt):
+    rng = np.random.default_rng(M + 11)
+    got, ref = _qmm_case(ops, rng, M, 256, 512, xdt, mode=mode)
+    assert rel_err(got, ref) <= TOL_FP[xdt]
+
+
+@pytest.mark.parametrize("xdt", ["bf16", "f32"])
+@pytest.mark.parametrize("M", [1, 6, 100])
+@pytest.mark.parametrize("mode,bits,gs", [("affine", 4, 64), ("affine", 3, 32),
+                                          ("affine", 8, 128), ("nvfp4", 4, 16),
+                                          ("mxfp8", 8, 32)])
+def test_qmm_no_transpose(ops, mode, bits, gs, M, xdt):
+    rng = np.random.default_rng(M + bits)
+    got, ref = _qmm_case(ops, rng, M, 256, 384, xdt, mode=mode, bits=bits, gs=gs,
+                         transpose=False)
+    tol = TOL if mode == "affine" else TOL_FP
+    assert rel_err(got, ref) <= tol[xdt]
+
+
+def test_qmm_ragged_edges(ops):
+    # N, M not multiples of any tile; K the minimum legal
+    for (M, N, K) in [(1, 1, 32), (2, 3, 64), (129, 131, 96), (9, 257, 160)]:
+        rng = np.random.default_rng(M * N)
+        got, ref = _qmm_case(ops, rng, M, N, K, "bf16", gs=32)
+        assert rel_err(got, ref) <= TOL["bf16"], (M, N, K)
+
+
+def test_qmm_batched_weight_broadcast(ops):
+    rng = np.random.default_rng(5)
+    B, M, N, K = 3, 4, 64, 256
+    w, s, b = rand_affine(rng, N, K, 64, 4, "bf16", lead=(B,))
+    x = oracle.from_float(rng.standard_normal((2, 1, M, K)).astype(np.float32), "bf16")
+    got = ops.quantized_matmul(from_np(x, "bf16"), words_to_torch(w), from_np(s, "bf16"),
+                               from_np(b, "bf16"), True, 64, 4)
+    assert tuple(got.shape) == (2, B, M, N)
+    g = as_f64(to_np(got, "bf16"), "bf16")
+    for i in range(2):
+        for j in range(B):
+            ref = oracle.qmm(x[i, 0], "bf16", w[j], s[j], b[j], "bf16", True, 64, 4, odt="f32")
+            assert rel_err(g[i, j], ref) <= TOL["bf16"]
+
+
+def test_qmm_leading_dims_fold(ops):
+    rng = np.random.default_rng(6)
+    w, s, b = rand_affine(rng, 96, 256, 64, 4, "f16")
+    x = oracle.from_float(rng.standard_normal((2, 5, 256)).astype(np.float32), "f16")
+    got = ops.quantized_matmul(from_np(x, "f16"), words_to_torch(w), from_np(s, "f16"),
+                               from_np(b, "f16"))
+    assert tuple(got.shape) == (2, 5, 96)
+    ref = oracle.qmm(x.reshape(10, 256), "f16", w, s, b, "f16", True, 64, 4, odt="f32")
+    assert rel_err(as_f64(to_np(got, "f16"), "f16").reshape(10, 96), ref) <= TOL["f16"]
+
+
+def test_qmm_empty_and_zero_k(ops):
+    rng = np.random.default_rng(0)
+    w, s, b = rand_affine(rng, 64, 128, 64, 4, "bf16")
+    x = torch.zeros((0, 128), dtype=torch.bfloat16, device="cuda")
+    out = ops.quantized_matmul(x, words_to_torch(w), from_np(s, "bf16"), from_np(b, "bf16"))
+    assert tuple(out.shape) == (0, 64)
+
+
+def test_qmm_errors_raise(ops):
+    from ironmlx_amd import IqmmError
+    rng = np.random.default_rng(0)
+    w, s, b = rand_affine(rng, 64, 128, 64, 4, "bf16")
+    x = torch.zeros((1, 128), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(IqmmError, match="Invalid quantization mode"):
+        ops.quantized_matmul(x, words_to_torch(w), from_np(s, "bf16"), from_np(b, "bf16"),
+                             mode="q4")
+    with pytest.raises(IqmmError, match="GPU only"):
+        ops.quantized_matmul(x.cpu(), words_to_torch(w), from_np(s, "bf16"), from_np(b, "bf16"))
+
+
+# ------------------------------------------------------------------ gather_qmm
+@pytest.mark.parametrize("sorted_idx", [False, True])
+@pytest.mark.parametrize("M", [1, 3, 20])
+def test_gather_qmm_vs_loop(ops, M, sorted_idx):
+    rng = np.random.default_rng(M + 40)
+    E, N, K, T, topk = 8, 64, 256, 6, 3
+    w, s, b = rand_affine(rng, N, K, 64, 4, "bf16", lead=(E,))
+    x = oracle.from_float(rng.standard_normal((T, 1, M, K)).astype(np.float32), "bf16")
+    idx = np.stack([rng.choice(E, topk, replace=False) for _ in range(T)]).astype(np.int32)
+    if sorted_idx:
+        # the sorted form: rows flattened and ordered by expert
+        flat = idx.reshape(-1)
+        order = np.argsort(flat, kind="stable")
+        xs = x.reshape(T, M, K)[order // topk]                # [T*topk, M, K]
+        got = ops.gather_qmm(from_np(xs, "bf16"), words_to_torch(w), from_np(s, "bf16"),
+                             from_np(b, "bf16"), None, torch.from_numpy(flat[order]).cuda(),
+                             sorted_indices=True)
+        assert tuple(got.shape) == (T * topk, M, N)
+        g = as_f64(to_np(got, "bf16"), "bf16")
+        for i, e in enumerate(flat[order]):
+            ref = oracle.qmm(xs[i], "bf16", w[e], s[e], b[e], "bf16", True, 64, 4, odt="f32")
+            assert rel_err(g[i], ref) <= TOL["bf16"]
+    else:
+        got = ops.gather_qmm(from_np(x, "bf16"), words_to_torch(w), from_np(s, "bf16"),
+                             from_np(b, "bf16"), None, torch.from_numpy(idx).cuda())
+        assert tuple(got.shape) == (T, topk, M, N)
+        ref = oracle.gather_qmm(x.reshape(T, M, K), "bf16", w, s, b, "bf16",
+                                np.broadcast_to(np.arange(T)[:, None], idx.shape), idx,
+                                odt="f32")
+        assert rel_err(as_f64(to_np(got, "bf16"), "bf16"), ref) <= TOL["bf16"]
+
+
+def test_gather_qmm_lhs_and_out_of_range(ops):
+    rng = np.random.default_rng(9)
+    E, N, K, M = 4, 64, 128, 2
+    w, s, b = rand_affine(rng, N, K, 32, 4, "f16", lead=(E,))
+    x = oracle.from_float(rng.standard_normal((5, M, K)).astype(np.float32), "f16")
+    lhs = np.array([0, 4, 2, 2], np.int64)
+    rhs = np.array([3, 0, 9, 1], np.uint32)          # 9 is out of range
+    got = ops.gather_qmm(from_np(x, "f16"), words_to_torch(w), from_np(s, "f16"),
+                         from_np(b, "f16"), torch.from_numpy(lhs).cuda(),
+                         torch.from_numpy(rhs.view(np.int32)).cuda().view(torch.uint32),
+                         group_size=32)
+    g = as_f64(to_np(got, "f16"), "f16")
+    for i in range(4):
+        if rhs[i] >= E:
+            assert np.all(np.isnan(g[i]))
+        else:
+            ref = oracle.qmm(x[lhs[i]], "f16", w[rhs[i]], s[rhs[i]], b[rhs[i]], "f16", True,
+                             32, 4, odt="f32")
+            assert rel_err(g[i], ref) <= TOL["f16"]
