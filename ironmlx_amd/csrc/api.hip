@@ -196,6 +196,7 @@ hipError_t fill_zero(void* p, int dt, int64_t n, hipStream_t st) {
 // choose the kernel family for one problem
 hipError_t run_qmm(QmmArgs& a) {
   if (qmv_q4_m1_supported(a)) return launch_qmv_q4_m1(a);
+  if (a.M >= 128 && a.nbatch <= 65535 && qmm_gemm_supported(a)) return launch_qmm_gemm(a);
   const bool small_m = a.M <= 8;
   if (!small_m && qmm_mfma_supported(a)) return launch_qmm_mfma(a);
   return a.transpose ? launch_qmv(a) : launch_qvm(a);

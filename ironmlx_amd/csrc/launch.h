@@ -47,6 +47,8 @@ bool qmv_q4_m1_supported(const QmmArgs& a);
 hipError_t launch_qvm(const QmmArgs& a);        // transpose=false, small M, VALU
 hipError_t launch_qmm_mfma(const QmmArgs& a);   // bf16/fp16 MFMA tiles, any M
 bool qmm_mfma_supported(const QmmArgs& a);
+hipError_t launch_qmm_gemm(const QmmArgs& a);   // 256x256 prefill GEMM
+bool qmm_gemm_supported(const QmmArgs& a);
 hipError_t launch_dequantize(const ConvArgs& a);
 hipError_t launch_quantize(const ConvArgs& a);
 
