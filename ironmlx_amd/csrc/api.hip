@@ -196,7 +196,9 @@ hipError_t fill_zero(void* p, int dt, int64_t n, hipStream_t st) {
 // choose the kernel family for one problem
 hipError_t run_qmm(QmmArgs& a) {
   if (qmv_q4_m1_supported(a)) return launch_qmv_q4_m1(a);
-  if (a.M >= 128 && a.nbatch <= 65535 && qmm_gemm_supported(a)) return launch_qmm_gemm(a);
+  if (a.M >= 2 && a.M <= 64 && a.nbatch * ((a.M + 31) / 32) <= 65535 && qmm_skinny_supported(a))
+    return launch_qmm_skinny(a);
+  if (a.M > 64 && a.nbatch <= 65535 && qmm_gemm_supported(a)) return launch_qmm_gemm(a);
   const bool small_m = a.M <= 8;
   if (!small_m && qmm_mfma_supported(a)) return launch_qmm_mfma(a);
   return a.transpose ? launch_qmv(a) : launch_qvm(a);
@@ -316,7 +318,6 @@ int iqmm_gather_qmm(iqmm_array* res, iqmm_array x, iqmm_array w, iqmm_array scal
                     bool sorted_indices, iqmm_stream stream) {
   const char* op = "gather_qmm";
   g_last_error.clear();
-  (void)sorted_indices;
   QParams q;
   if (resolve(op, mode, group_size, bits, q)) return 1;
   if (!present(x) || x.ndim < 2) return fail("[%s] x must have at least two dimensions.", op);
@@ -364,6 +365,14 @@ int iqmm_gather_qmm(iqmm_array* res, iqmm_array x, iqmm_array w, iqmm_array scal
   a.bm.rhs = present(rhs) ? rhs.data : nullptr;
   a.bm.lhs_dt = lhs.dtype; a.bm.rhs_dt = rhs.dtype;
   a.stream = st;
+  // sorted form: rhs (and lhs, or x's batch when lhs is absent) enumerate the
+  // output batch one-to-one, so expert segments are contiguous in it
+  const bool one_to_one = present(rhs) && numel(rhs) == a.nbatch &&
+                          (present(lhs) ? numel(lhs) == a.nbatch : nxm == a.nbatch);
+  if (sorted_indices && one_to_one && gather_sorted_supported(a) && nwm + 1 <= 65535) {
+    hipError_t e = launch_gather_sorted(a, a.nbatch, nwm);
+    return e == hipSuccess ? 0 : hip_fail(op, e);
+  }
   hipError_t e = run_qmm(a);
   return e == hipSuccess ? 0 : hip_fail(op, e);
 }

@@ -48,6 +48,11 @@ hipError_t launch_qvm(const QmmArgs& a);        // transpose=false, small M, VAL
 hipError_t launch_qmm_mfma(const QmmArgs& a);   // bf16/fp16 MFMA tiles, any M
 bool qmm_mfma_supported(const QmmArgs& a);
 hipError_t launch_qmm_gemm(const QmmArgs& a);   // 256x256 prefill GEMM
+hipError_t launch_qmm_skinny(const QmmArgs& a); // decode widths 2 <= M <= 64
+bool qmm_skinny_supported(const QmmArgs& a);
+// sorted-expert grouped gather_qmm: nflat batch elements, E experts
+hipError_t launch_gather_sorted(const QmmArgs& a, int64_t nflat, int64_t E);
+bool gather_sorted_supported(const QmmArgs& a);
 bool qmm_gemm_supported(const QmmArgs& a);
 hipError_t launch_dequantize(const ConvArgs& a);
 hipError_t launch_quantize(const ConvArgs& a);

@@ -1,0 +1,741 @@
+// qmm_skinny.hip — decode-width quantized matmul (transpose=true, 2 <= M <= 64)
+// on CDNA4 matrix cores.
+//
+// The batched-decode widths (M in {4, 8, 16, 32} for continuous batching) are
+// still HBM-bound on the weights, but far too much arithmetic for the
+// vector-ALU GEMV.  A workgroup owns 32 weight rows; its S waves split K.
+// Per 64-code block p, lane l = (n = l % 32, h = l / 32) streams the 16-byte
+// chunk 2p + h of row n (one coalesced 32-byte run per row per wave), reads
+// that chunk's scale/bias, dequantizes the 32 codes in registers (the
+// `dequantize` arithmetic, so every group size and mode works) and feeds
+// them as the B operand of four v_mfma_f32_32x32x16 (code 8j..8j+7 to MFMA
+// j).  The A operand is x rows m = l % 32 (16-byte loads of the matching k
+// positions; rows >= M read as zero).  Each wave leaves a 32 x 32 fp32
+// partial; the S partials are summed through LDS and rows < M are stored.
+// Reference op: mlx/src/ops.rs:695-727 with x = [B, 1, K] (one decode step
+// for B sequences, which mlx/src/generate/batch.rs:313-339 runs as B
+// separate M = 1 calls today).
+#include <stdlib.h>
+
+#include "launch.h"
+#include "mfma_common.h"
+
+namespace iqmm {
+
+constexpr int SK_ROWS = 32;
+
+template <int XT, int MODE, int BITS, int S, int U>
+__global__ __launch_bounds__(64 * S) void qmm_skinny_kernel(QmmArgs a, int nmt) {
+  using XS = uint16_t;
+  constexpr bool AFF = MODE == AFFINE;
+  __shared__ float red[S * 32 * 33];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int M = a.M, N = a.N, K = a.K;
+  const int n0 = blockIdx.x * SK_ROWS;
+  const int mt = blockIdx.y % nmt;
+  const int64_t bb = blockIdx.y / nmt;
+  const int m0 = mt * 32;
+  XS* out = static_cast<XS*>(a.out) + bb * static_cast<int64_t>(M) * N;
+
+  int64_t xb = 0, wb = 0;
+  if (a.bm.ndim != 0 || a.bm.lhs != nullptr || a.bm.rhs != nullptr) {
+    if (!map_batch(a.bm, bb, xb, wb)) {
+      for (int i = t; i < 32 * SK_ROWS; i += 64 * S) {
+        const int r = m0 + i / SK_ROWS, c = n0 + i % SK_ROWS;
+        if (r < M && c < N) out[static_cast<int64_t>(r) * N + c] = from_f<XT>(__builtin_nanf(""));
+      }
+      return;
+    }
+  }
+  const XS* x = static_cast<const XS*>(a.x) + xb * a.x_mat;
+  const uint32_t* w = a.w + wb * a.w_mat;
+  const int gs = AFF ? a.gs : ModeInfo<MODE>::GS;
+  const int G = K / gs;
+  const XS* sp = static_cast<const XS*>(a.s) + wb * a.s_mat;
+  const XS* bp = AFF ? static_cast<const XS*>(a.b) + wb * a.s_mat : nullptr;
+  const uint8_t* s8 = static_cast<const uint8_t*>(a.s) + wb * a.s_mat;
+  const int64_t wpr = static_cast<int64_t>(K) * BITS / 32;
+
+  const int nl = lane & 31, h = lane >> 5;
+  const int row = min(n0 + nl, N - 1);
+  const uint32_t* wrow = w + static_cast<int64_t>(row) * wpr;
+  const int xm = m0 + nl;                      // this lane's x row (A operand)
+  const bool xvalid = xm < M;
+  const XS* xrow = x + static_cast<int64_t>(xvalid ? xm : 0) * K;
+
+  // K blocks of 64 codes split evenly over the S waves
+  const int P = K >> 6;
+  const int pb = (P * wave) / S, pe = (P * (wave + 1)) / S;
+
+  f32x16_t acc;
+#pragma unroll
+  for (int v = 0; v < 16; ++v) acc[v] = 0.f;
+
+  // U blocks per batch: all loads of the batch are issued before any
+  // dequantization, so U x (16 B of W + 64 B of x) per lane are in flight
+  struct Blk {
+    uint32_t wd[BITS];
+    float s, b, s2;
+    g_u32x4_t xa[4];
+  };
+  auto load = [&](int p, Blk& B) {
+    const int c = 2 * min(p, pe - 1) + h;
+    load_chunk<BITS>(B.wd, wrow + c * BITS);
+    const int gi = (c * 32) / gs;
+    if constexpr (AFF) {
+      B.s = to_f<XT>(sp[static_cast<int64_t>(row) * G + gi]);
+      B.b = to_f<XT>(bp[static_cast<int64_t>(row) * G + gi]);
+      B.s2 = B.s;
+    } else {
+      B.s = fp_scale<MODE>(s8[static_cast<int64_t>(row) * G + gi]);
+      B.b = 0.f;
+      B.s2 = MODE == NVFP4 ? fp_scale<MODE>(s8[static_cast<int64_t>(row) * G + gi + 1]) : B.s;
+    }
+    const g_u32x4_t* xp = reinterpret_cast<const g_u32x4_t*>(xrow + c * 32);
+    const bool live = xvalid && p < pe;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) B.xa[j] = live ? xp[j] : g_u32x4_t{0, 0, 0, 0};
+  };
+  auto compute = [&](const Blk& B) {
+    uint32_t o[16];
+    dequant32<XT, MODE, BITS>(B.wd, B.s, B.b, B.s2, o);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      acc = mfma32<XT>(B.xa[j], g_u32x4_t{o[4 * j], o[4 * j + 1], o[4 * j + 2], o[4 * j + 3]}, acc);
+  };
+  for (int p = pb; p < pe; p += U) {
+    Blk B[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) load(p + u, B[u]);
+#pragma unroll
+    for (int u = 0; u < U; ++u) compute(B[u]);   // blocks past pe carry x = 0
+  }
+
+  // lane holds C[m = 8(v/4) + 4h + v%4][n = nl]
+#pragma unroll
+  for (int v = 0; v < 16; ++v) {
+    const int m = 8 * (v >> 2) + 4 * h + (v & 3);
+    red[(wave * 32 + m) * 33 + nl] = acc[v];
+  }
+  __syncthreads();
+  for (int i = t; i < 32 * SK_ROWS; i += 64 * S) {
+    const int m = i / SK_ROWS, n = i % SK_ROWS;
+    float v = 0.f;
+#pragma unroll
+    for (int w2 = 0; w2 < S; ++w2) v += red[(w2 * 32 + m) * 33 + n];
+    if (m0 + m < M && n0 + n < N) out[static_cast<int64_t>(m0 + m) * N + n0 + n] = from_f<XT>(v);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Factored variant for affine 4-bit with group_size >= 64 (the common case).
+// In the layout above one 64-code block of a row is exactly one quantization
+// group, so the codes go to the MFMA unconverted: v_perm_b32 against a byte
+// register of 0x43 (bf16) / 0x64 (fp16) turns nibble pairs into the exact
+// 16-bit values C + q (C = 128 / 1024), and per block
+//   acc += s * sum x (C + q)  +  (b - C s) * sum x
+// where sum x over the block comes from one more MFMA chain against ones.
+// x is permuted to the nibble-pair order (n0,n4)(n2,n6)(n1,n5)(n3,n7) of each
+// word.  MT = number of 8-row groups of the 32-row tile that hold rows < M
+// (the epilogue only touches those accumulators).
+template <int XT, int S, int MT>
+__global__ __launch_bounds__(64 * S) void qmm_skinny_q4f_kernel(QmmArgs a, int nmt) {
+  using XS = uint16_t;
+  __shared__ float red[S * 32 * 33];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int M = a.M, N = a.N, K = a.K;
+  const int n0 = blockIdx.x * SK_ROWS;
+  const int mt = blockIdx.y % nmt;
+  const int64_t bb = blockIdx.y / nmt;
+  const int m0 = mt * 32;
+  XS* out = static_cast<XS*>(a.out) + bb * static_cast<int64_t>(M) * N;
+  int64_t xb = 0, wb = 0;
+  if (a.bm.ndim != 0 || a.bm.lhs != nullptr || a.bm.rhs != nullptr) {
+    if (!map_batch(a.bm, bb, xb, wb)) {
+      for (int i = t; i < 32 * SK_ROWS; i += 64 * S) {
+        const int r = m0 + i / SK_ROWS, c = n0 + i % SK_ROWS;
+        if (r < M && c < N) out[static_cast<int64_t>(r) * N + c] = from_f<XT>(__builtin_nanf(""));
+      }
+      return;
+    }
+  }
+  const XS* x = static_cast<const XS*>(a.x) + xb * a.x_mat;
+  const uint32_t* w = a.w + wb * a.w_mat;
+  const int G = K / a.gs, gshift = __builtin_ctz(a.gs);
+  const XS* sp = static_cast<const XS*>(a.s) + wb * a.s_mat;
+  const XS* bp = static_cast<const XS*>(a.b) + wb * a.s_mat;
+  const int64_t wpr = K >> 3;
+  const int nl = lane & 31, h = lane >> 5;
+  const int row = min(n0 + nl, N - 1);
+  const uint32_t* wrow = w + static_cast<int64_t>(row) * wpr;
+  const XS* srow = sp + static_cast<int64_t>(row) * G;
+  const XS* brow = bp + static_cast<int64_t>(row) * G;
+  const int xm = m0 + nl;
+  const bool xvalid = xm < M;
+  const XS* xrow = x + static_cast<int64_t>(xvalid ? xm : 0) * K;
+  const int P = K >> 6;
+  const int pb = (P * wave) / S, pe = (P * (wave + 1)) / S;
+  constexpr uint32_t E = XT == BF16 ? 0x43434343u : 0x64646464u;
+  constexpr float C = XT == BF16 ? 128.f : 1024.f;
+  constexpr uint32_t ONE2 = XT == BF16 ? 0x3f803f80u : 0x3c003c00u;
+  const g_u32x4_t ones = {ONE2, ONE2, ONE2, ONE2};
+
+  f32x16_t acc;
+#pragma unroll
+  for (int v = 0; v < 16; ++v) acc[v] = 0.f;
+
+  struct Blk {
+    g_u32x4_t wv;
+    XS s, b;
+    g_u32x4_t xa[4];
+  };
+  auto load = [&](int p, Blk& B) {
+    const int pc = min(p, pe - 1);
+    const int c = 2 * pc + h;
+    B.wv = __builtin_nontemporal_load(reinterpret_cast<const g_u32x4_t*>(wrow + c * 4));
+    const int g = (pc << 6) >> gshift;
+    B.s = srow[g];
+    B.b = brow[g];
+    const g_u32x4_t* xp = reinterpret_cast<const g_u32x4_t*>(xrow + c * 32);
+    const bool live = xvalid && p < pe;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) B.xa[j] = live ? xp[j] : g_u32x4_t{0, 0, 0, 0};
+  };
+  auto compute = [&](const Blk& B) {
+    f32x16_t tq, t1;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) { tq[v] = 0.f; t1[v] = 0.f; }
+    const uint32_t wd[4] = {B.wv.x, B.wv.y, B.wv.z, B.wv.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t lo = wd[j] & 0x0F0F0F0Fu, hi = (wd[j] >> 4) & 0x0F0F0F0Fu;
+      const g_u32x4_t q = {__builtin_amdgcn_perm(E, lo, 0x04020400u),   // n0, n4
+                           __builtin_amdgcn_perm(E, lo, 0x04030401u),   // n2, n6
+                           __builtin_amdgcn_perm(E, hi, 0x04020400u),   // n1, n5
+                           __builtin_amdgcn_perm(E, hi, 0x04030401u)};  // n3, n7
+      const g_u32x4_t xv = B.xa[j];   // x0..x7 as pairs (x0x1)(x2x3)(x4x5)(x6x7)
+      const g_u32x4_t xq = {__builtin_amdgcn_perm(xv.z, xv.x, 0x05040100u),   // x0, x4
+                            __builtin_amdgcn_perm(xv.w, xv.y, 0x05040100u),   // x2, x6
+                            __builtin_amdgcn_perm(xv.z, xv.x, 0x07060302u),   // x1, x5
+                            __builtin_amdgcn_perm(xv.w, xv.y, 0x07060302u)};  // x3, x7
+      tq = mfma32<XT>(xq, q, tq);
+      t1 = mfma32<XT>(xv, ones, t1);
+    }
+    const float s = to_f<XT>(B.s), b = to_f<XT>(B.b);
+    const float bc = fmaf(-C, s, b);
+#pragma unroll
+    for (int v = 0; v < 4 * MT; ++v) acc[v] = fmaf(s, tq[v], fmaf(bc, t1[v], acc[v]));
+  };
+  for (int p = pb; p < pe; p += 2) {
+    Blk B0, B1;
+    load(p, B0);
+    load(p + 1, B1);
+    compute(B0);
+    if (p + 1 < pe) compute(B1);
+  }
+#pragma unroll
+  for (int v = 0; v < 16; ++v) {
+    const int m = 8 * (v >> 2) + 4 * h + (v & 3);
+    red[(wave * 32 + m) * 33 + nl] = acc[v];
+  }
+  __syncthreads();
+  for (int i = t; i < 32 * SK_ROWS; i += 64 * S) {
+    const int m = i / SK_ROWS, n = i % SK_ROWS;
+    float v = 0.f;
+#pragma unroll
+    for (int w2 = 0; w2 < S; ++w2) v += red[(w2 * 32 + m) * 33 + n];
+    if (m0 + m < M && n0 + n < N) out[static_cast<int64_t>(m0 + m) * N + n0 + n] = from_f<XT>(v);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 16x16x32 variant: lane l = (n = l % 16, q = l / 16) streams chunk 4p + q of
+// row n, so each wave instruction reads 16 rows x 64 contiguous bytes (the
+// 32x32 layout's 32-byte runs leave half-used 128-byte lines behind).  The 32
+// codes are dequantized in registers and feed four v_mfma_f32_16x16x32 per
+// 16-row x-tile (word j -> MFMA j; x positions 128p + 32q + 8j .. +8).
+typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+
+template <int XT>
+__device__ __forceinline__ f32x4_t mfma16x(const g_u32x4_t& a, const g_u32x4_t& b, const f32x4_t& c) {
+  if constexpr (XT == BF16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(g_bf16x8_t, a),
+                                                   __builtin_bit_cast(g_bf16x8_t, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(g_f16x8_t, a),
+                                                  __builtin_bit_cast(g_f16x8_t, b), c, 0, 0, 0);
+}
+
+// byte k of v as fp32 (v_cvt_f32_ubyte{k})
+template <int B>
+__device__ __forceinline__ float ubyte_f(uint32_t v) {
+  float r;
+  if constexpr (B == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(v));
+  else if constexpr (B == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(v));
+  else if constexpr (B == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(v));
+  else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(v));
+  return r;
+}
+
+// affine 4-bit chunk -> 16 packed pairs in natural order
+template <int XT>
+__device__ __forceinline__ void deq4_fast(const g_u32x4_t& wv, float s, float b, uint32_t (&o)[16]) {
+  const uint32_t wd[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const uint32_t lo = wd[q] & 0x0F0F0F0Fu, hi = (wd[q] >> 4) & 0x0F0F0F0Fu;
+    o[4 * q + 0] = pack2<XT>(fmaf(s, ubyte_f<0>(lo), b), fmaf(s, ubyte_f<0>(hi), b));
+    o[4 * q + 1] = pack2<XT>(fmaf(s, ubyte_f<1>(lo), b), fmaf(s, ubyte_f<1>(hi), b));
+    o[4 * q + 2] = pack2<XT>(fmaf(s, ubyte_f<2>(lo), b), fmaf(s, ubyte_f<2>(hi), b));
+    o[4 * q + 3] = pack2<XT>(fmaf(s, ubyte_f<3>(lo), b), fmaf(s, ubyte_f<3>(hi), b));
+  }
+}
+
+template <int XT, int MODE, int BITS, int S, int MT, int U>
+__global__ __launch_bounds__(64 * S) void qmm_skinny16_kernel(QmmArgs a, int nmt) {
+  using XS = uint16_t;
+  constexpr bool AFF = MODE == AFFINE;
+  __shared__ float red[S * 32 * 17];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int M = a.M, N = a.N, K = a.K;
+  const int n0 = blockIdx.x * 16;
+  const int mt = blockIdx.y % nmt;
+  const int64_t bb = blockIdx.y / nmt;
+  const int m0 = mt * 32;
+  XS* out = static_cast<XS*>(a.out) + bb * static_cast<int64_t>(M) * N;
+  int64_t xb = 0, wb = 0;
+  if (a.bm.ndim != 0 || a.bm.lhs != nullptr || a.bm.rhs != nullptr) {
+    if (!map_batch(a.bm, bb, xb, wb)) {
+      for (int i = t; i < 32 * 16; i += 64 * S) {
+        const int r = m0 + i / 16, c = n0 + i % 16;
+        if (r < M && c < N) out[static_cast<int64_t>(r) * N + c] = from_f<XT>(__builtin_nanf(""));
+      }
+      return;
+    }
+  }
+  const XS* x = static_cast<const XS*>(a.x) + xb * a.x_mat;
+  const uint32_t* w = a.w + wb * a.w_mat;
+  const int gs = AFF ? a.gs : ModeInfo<MODE>::GS;
+  const int G = K / gs;
+  const XS* sp = static_cast<const XS*>(a.s) + wb * a.s_mat;
+  const XS* bp = AFF ? static_cast<const XS*>(a.b) + wb * a.s_mat : nullptr;
+  const uint8_t* s8 = static_cast<const uint8_t*>(a.s) + wb * a.s_mat;
+  const int64_t wpr = static_cast<int64_t>(K) * BITS / 32;
+  const int nl = lane & 15, q = lane >> 4;
+  const int row = min(n0 + nl, N - 1);
+  const uint32_t* wrow = w + static_cast<int64_t>(row) * wpr;
+  // x rows for the MT 16-row tiles: lane feeds row m0 + 16 i + nl
+  const XS* xrows[MT];
+  bool xv[MT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i) {
+    const int xm = m0 + 16 * i + nl;
+    xv[i] = xm < M;
+    xrows[i] = x + static_cast<int64_t>(xv[i] ? xm : 0) * K;
+  }
+  const int P = K >> 7;   // 128-code blocks
+  const int pb = (P * wave) / S, pe = (P * (wave + 1)) / S;
+  f32x4_t acc[MT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i) acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  struct Blk {
+    uint32_t wd[BITS];
+    float s, b, s2;
+    g_u32x4_t xa[MT][4];
+  };
+  auto load = [&](int p, Blk& B) {
+    const int pc = min(p, pe - 1);
+    const int c = 4 * pc + q;
+    load_chunk<BITS>(B.wd, wrow + c * BITS);
+    const int gi = (c * 32) / gs;
+    if constexpr (AFF) {
+      B.s = to_f<XT>(sp[static_cast<int64_t>(row) * G + gi]);
+      B.b = to_f<XT>(bp[static_cast<int64_t>(row) * G + gi]);
+      B.s2 = B.s;
+    } else {
+      B.s = fp_scale<MODE>(s8[static_cast<int64_t>(row) * G + gi]);
+      B.b = 0.f;
+      B.s2 = MODE == NVFP4 ? fp_scale<MODE>(s8[static_cast<int64_t>(row) * G + gi + 1]) : B.s;
+    }
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+      const g_u32x4_t* xp = reinterpret_cast<const g_u32x4_t*>(xrows[i] + c * 32);
+      const bool live = xv[i] && p < pe;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) B.xa[i][j] = live ? xp[j] : g_u32x4_t{0, 0, 0, 0};
+    }
+  };
+  auto compute = [&](const Blk& B) {
+    uint32_t o[16];
+    if constexpr (AFF && BITS == 4)
+      deq4_fast<XT>(g_u32x4_t{B.wd[0], B.wd[1], B.wd[2], B.wd[3]}, B.s, B.b, o);
+    else
+      dequant32<XT, MODE, BITS>(B.wd, B.s, B.b, B.s2, o);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const g_u32x4_t wb4 = {o[4 * j], o[4 * j + 1], o[4 * j + 2], o[4 * j + 3]};
+#pragma unroll
+      for (int i = 0; i < MT; ++i) acc[i] = mfma16x<XT>(B.xa[i][j], wb4, acc[i]);
+    }
+  };
+  for (int p = pb; p < pe; p += U) {
+    Blk B[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) load(p + u, B[u]);
+#pragma unroll
+    for (int u = 0; u < U; ++u) compute(B[u]);   // blocks past pe carry x = 0
+  }
+  // lane holds C[4 q + r][nl] of each 16 x 16 tile i
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[(wave * 32 + 16 * i + 4 * q + r) * 17 + nl] = acc[i][r];
+  __syncthreads();
+  for (int i = t; i < 16 * MT * 16; i += 64 * S) {
+    const int m = i / 16, n = i % 16;
+    float v = 0.f;
+#pragma unroll
+    for (int w2 = 0; w2 < S; ++w2) v += red[(w2 * 32 + m) * 17 + n];
+    if (m0 + m < M && n0 + n < N) out[static_cast<int64_t>(m0 + m) * N + n0 + n] = from_f<XT>(v);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Grouped gather_qmm for sorted expert indices (mlx-c gather_qmm with
+// sorted_indices = true; the MoE layer of mlx/src/nn/moe.rs:84-170 over the
+// stacked [E, N, K/pack] expert tensors of mlx/src/model/qwen35.rs:653-775).
+// blockIdx.y = expert e.  The workgroup binary-searches the sorted flat rhs
+// index array for its row segment [lo, hi), so each expert's weight rows are
+// read once for all of the tokens routed to it (in 32-row m tiles).  Segment
+// row r is batch element b = lo + r / Mx, matrix row r % Mx, x matrix lhs[b].
+template <int XT, int MODE, int BITS, int S>
+__global__ __launch_bounds__(64 * S) void gather_sorted_kernel(QmmArgs a, int64_t nflat) {
+  using XS = uint16_t;
+  constexpr bool AFF = MODE == AFFINE;
+  constexpr int MT = 2;
+  __shared__ float red[S * 32 * 17];
+  __shared__ int64_t seg[2];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int Mx = a.M, N = a.N, K = a.K;
+  const int n0 = blockIdx.x * 16;
+  const int64_t e = blockIdx.y;
+  if (e == a.bm.nw) {
+    // the extra block row: batch elements whose expert index is out of
+    // [0, E) get NaN rows (they belong to no expert segment)
+    int64_t lo = 0, hi = nflat;
+    while (lo < hi) {
+      const int64_t mid = (lo + hi) >> 1;
+      if (load_index(a.bm.rhs, a.bm.rhs_dt, mid) < 0) lo = mid + 1; else hi = mid;
+    }
+    const int64_t first_valid = lo;
+    hi = nflat;
+    while (lo < hi) {
+      const int64_t mid = (lo + hi) >> 1;
+      if (load_index(a.bm.rhs, a.bm.rhs_dt, mid) < e) lo = mid + 1; else hi = mid;
+    }
+    const int64_t end_valid = lo;
+    XS* o = static_cast<XS*>(a.out);
+    const int64_t nbad = first_valid + (nflat - end_valid);
+    for (int64_t i = t; i < nbad * Mx * 16; i += 64 * S) {
+      const int64_t rr = i / 16, n = i % 16;
+      const int64_t bi = rr / Mx, mrow = rr % Mx;
+      const int64_t b = bi < first_valid ? bi : end_valid + (bi - first_valid);
+      if (n0 + n < N) o[(b * Mx + mrow) * N + n0 + n] = from_f<XT>(__builtin_nanf(""));
+    }
+    return;
+  }
+  if (t == 0) {
+    // lower_bound(e), lower_bound(e + 1) over the sorted flat rhs indices
+    int64_t lo = 0, hi = nflat;
+    while (lo < hi) {
+      const int64_t mid = (lo + hi) >> 1;
+      if (load_index(a.bm.rhs, a.bm.rhs_dt, mid) < e) lo = mid + 1; else hi = mid;
+    }
+    int64_t lo2 = lo, hi2 = nflat;
+    while (lo2 < hi2) {
+      const int64_t mid = (lo2 + hi2) >> 1;
+      if (load_index(a.bm.rhs, a.bm.rhs_dt, mid) <= e) lo2 = mid + 1; else hi2 = mid;
+    }
+    seg[0] = lo;
+    seg[1] = lo2;
+  }
+  __syncthreads();
+  const int64_t blo = seg[0], bhi = seg[1];
+  if (blo >= bhi) return;
+  const int64_t rows_total = (bhi - blo) * Mx;
+  XS* out = static_cast<XS*>(a.out);
+  const XS* x = static_cast<const XS*>(a.x);
+  const uint32_t* w = a.w + e * a.w_mat;
+  const int gs = AFF ? a.gs : ModeInfo<MODE>::GS;
+  const int G = K / gs;
+  const XS* sp = static_cast<const XS*>(a.s) + e * a.s_mat;
+  const XS* bp = AFF ? static_cast<const XS*>(a.b) + e * a.s_mat : nullptr;
+  const uint8_t* s8 = static_cast<const uint8_t*>(a.s) + e * a.s_mat;
+  const int64_t wpr = static_cast<int64_t>(K) * BITS / 32;
+  const int nl = lane & 15, q = lane >> 4;
+  const int row = min(n0 + nl, N - 1);
+  const uint32_t* wrow = w + static_cast<int64_t>(row) * wpr;
+  const int P = K >> 7;
+  const int pb = (P * wave) / S, pe = (P * (wave + 1)) / S;
+
+  for (int64_t r0 = 0; r0 < rows_total; r0 += 32) {
+    // this lane's x rows (A operand) for the two 16-row tiles
+    const XS* xrows[MT];
+    bool xv[MT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+      const int64_t r = r0 + 16 * i + nl;
+      xv[i] = r < rows_total;
+      const int64_t b = blo + (xv[i] ? r : 0) / Mx;
+      const int64_t mrow = (xv[i] ? r : 0) % Mx;
+      const int64_t xm = a.bm.lhs ? load_index(a.bm.lhs, a.bm.lhs_dt, b) : b;
+      const bool inb = xm >= 0 && xm < a.bm.nx;
+      xv[i] = xv[i] && inb;
+      xrows[i] = x + (inb ? xm : 0) * a.x_mat + mrow * K;
+    }
+    f32x4_t acc[MT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int p = pb; p < pe; ++p) {
+      const int c = 4 * p + q;
+      uint32_t wd[BITS];
+      load_chunk<BITS>(wd, wrow + c * BITS);
+      const int gi = (c * 32) / gs;
+      float sv, bv = 0.f, s2;
+      if constexpr (AFF) {
+        sv = to_f<XT>(sp[static_cast<int64_t>(row) * G + gi]);
+        bv = to_f<XT>(bp[static_cast<int64_t>(row) * G + gi]);
+        s2 = sv;
+      } else {
+        sv = fp_scale<MODE>(s8[static_cast<int64_t>(row) * G + gi]);
+        s2 = MODE == NVFP4 ? fp_scale<MODE>(s8[static_cast<int64_t>(row) * G + gi + 1]) : sv;
+      }
+      g_u32x4_t xa[MT][4];
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        const g_u32x4_t* xp = reinterpret_cast<const g_u32x4_t*>(xrows[i] + c * 32);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xa[i][j] = xv[i] ? xp[j] : g_u32x4_t{0, 0, 0, 0};
+      }
+      uint32_t o[16];
+      if constexpr (AFF && BITS == 4)
+        deq4_fast<XT>(g_u32x4_t{wd[0], wd[1], wd[2], wd[3]}, sv, bv, o);
+      else
+        dequant32<XT, MODE, BITS>(wd, sv, bv, s2, o);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const g_u32x4_t wb4 = {o[4 * j], o[4 * j + 1], o[4 * j + 2], o[4 * j + 3]};
+#pragma unroll
+        for (int i = 0; i < MT; ++i) acc[i] = mfma16x<XT>(xa[i][j], wb4, acc[i]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) red[(wave * 32 + 16 * i + 4 * q + rr) * 17 + nl] = acc[i][rr];
+    __syncthreads();
+    for (int i = t; i < 32 * 16; i += 64 * S) {
+      const int m = i / 16, n = i % 16;
+      const int64_t r = r0 + m;
+      if (r < rows_total && n0 + n < N) {
+        float v = 0.f;
+#pragma unroll
+        for (int w2 = 0; w2 < S; ++w2) v += red[(w2 * 32 + m) * 17 + n];
+        const int64_t b = blo + r / Mx, mrow = r % Mx;
+        const int64_t xm = a.bm.lhs ? load_index(a.bm.lhs, a.bm.lhs_dt, b) : b;
+        const bool inb = xm >= 0 && xm < a.bm.nx;
+        out[(b * Mx + mrow) * N + n0 + n] = from_f<XT>(inb ? v : __builtin_nanf(""));
+      }
+    }
+    __syncthreads();
+  }
+}
+
+bool gather_sorted_supported(const QmmArgs& a) {
+  return a.transpose && (a.xdt == BF16 || a.xdt == F16) && a.K % 128 == 0 && a.bm.rhs != nullptr;
+}
+
+bool qmm_skinny_supported(const QmmArgs& a) {
+  return a.transpose && (a.xdt == BF16 || a.xdt == F16) && a.K % 64 == 0 && a.M <= 64;
+}
+
+namespace {
+template <int XT, int MODE, int BITS>
+hipError_t skinny_launch_t(const QmmArgs& a) {
+  const int64_t ntiles = (a.N + SK_ROWS - 1) / SK_ROWS;
+  const int nmt = (a.M + 31) / 32;
+  const int64_t ny = static_cast<int64_t>(nmt) * a.nbatch;
+  if (ntiles <= 0 || ny <= 0) return hipSuccess;
+  if (ntiles > 0x7fffffffLL || ny > 65535) return hipErrorInvalidConfiguration;
+  // split K over S waves so that about 2048+ waves are in flight
+  const int P = a.K >> 6;
+  const int64_t tiles = ntiles * ny;
+  int S = 4;
+  if (tiles * 4 < 4096 && P >= 32) S = 8;
+  if (tiles * 8 < 4096 && P >= 64) S = 16;
+  static const int tuneS = [] { const char* e = getenv("IQMM_TUNE_SK_S"); return e ? atoi(e) : 0; }();
+  static const int tuneU = [] { const char* e = getenv("IQMM_TUNE_SK_U"); return e ? atoi(e) : 0; }();
+  if (tuneS) S = tuneS;
+  const int U = tuneU ? tuneU : 4;
+  const dim3 grid(static_cast<unsigned>(ntiles), static_cast<unsigned>(ny));
+#define IQMM_SK(SS, UU) hipLaunchKernelGGL((qmm_skinny_kernel<XT, MODE, BITS, SS, UU>), grid, dim3(64 * SS), 0, a.stream, a, nmt)
+  if (U == 2) {
+    switch (S) { case 16: IQMM_SK(16, 2); break; case 8: IQMM_SK(8, 2); break; default: IQMM_SK(4, 2); break; }
+  } else {
+    switch (S) { case 16: IQMM_SK(16, 4); break; case 8: IQMM_SK(8, 4); break; default: IQMM_SK(4, 4); break; }
+  }
+#undef IQMM_SK
+  return hipGetLastError();
+}
+
+template <int XT, int S>
+hipError_t q4f_launch_s(const QmmArgs& a, dim3 grid, int nmt) {
+  // MT: 8-row groups of the 32-row tile that carry rows < M
+  const int rows = a.M >= 32 ? 32 : a.M;
+  const int mtier = rows <= 8 ? 1 : rows <= 16 ? 2 : 4;
+  switch (mtier) {
+    case 1: hipLaunchKernelGGL((qmm_skinny_q4f_kernel<XT, S, 1>), grid, dim3(64 * S), 0, a.stream, a, nmt); break;
+    case 2: hipLaunchKernelGGL((qmm_skinny_q4f_kernel<XT, S, 2>), grid, dim3(64 * S), 0, a.stream, a, nmt); break;
+    default: hipLaunchKernelGGL((qmm_skinny_q4f_kernel<XT, S, 4>), grid, dim3(64 * S), 0, a.stream, a, nmt); break;
+  }
+  return hipGetLastError();
+}
+
+template <int XT>
+hipError_t q4f_launch(const QmmArgs& a) {
+  const int64_t ntiles = (a.N + SK_ROWS - 1) / SK_ROWS;
+  const int nmt = (a.M + 31) / 32;
+  const int64_t ny = static_cast<int64_t>(nmt) * a.nbatch;
+  if (ntiles <= 0 || ny <= 0) return hipSuccess;
+  if (ntiles > 0x7fffffffLL || ny > 65535) return hipErrorInvalidConfiguration;
+  const int P = a.K >> 6;
+  const int64_t tiles = ntiles * ny;
+  int S = 4;
+  if (tiles * 4 < 4096 && P >= 32) S = 8;
+  if (tiles * 8 < 4096 && P >= 64) S = 16;
+  static const int tuneS = [] { const char* e = getenv("IQMM_TUNE_SK_S"); return e ? atoi(e) : 0; }();
+  if (tuneS) S = tuneS;
+  const dim3 grid(static_cast<unsigned>(ntiles), static_cast<unsigned>(ny));
+  switch (S) {
+    case 16: return q4f_launch_s<XT, 16>(a, grid, nmt);
+    case 8: return q4f_launch_s<XT, 8>(a, grid, nmt);
+    default: return q4f_launch_s<XT, 4>(a, grid, nmt);
+  }
+}
+
+template <int XT, int MODE, int BITS, int S>
+hipError_t s16_launch_s(const QmmArgs& a, dim3 grid, int nmt) {
+  const int rows = a.M >= 32 ? 32 : a.M;
+  static const int tuneU = [] { const char* e = getenv("IQMM_TUNE_SK_U"); return e ? atoi(e) : 4; }();
+  if (tuneU == 8) {
+    if (rows <= 16) hipLaunchKernelGGL((qmm_skinny16_kernel<XT, MODE, BITS, S, 1, 8>), grid, dim3(64 * S), 0, a.stream, a, nmt);
+    else hipLaunchKernelGGL((qmm_skinny16_kernel<XT, MODE, BITS, S, 2, 8>), grid, dim3(64 * S), 0, a.stream, a, nmt);
+  } else if (tuneU == 2) {
+    if (rows <= 16) hipLaunchKernelGGL((qmm_skinny16_kernel<XT, MODE, BITS, S, 1, 2>), grid, dim3(64 * S), 0, a.stream, a, nmt);
+    else hipLaunchKernelGGL((qmm_skinny16_kernel<XT, MODE, BITS, S, 2, 2>), grid, dim3(64 * S), 0, a.stream, a, nmt);
+  } else {
+    if (rows <= 16) hipLaunchKernelGGL((qmm_skinny16_kernel<XT, MODE, BITS, S, 1, 4>), grid, dim3(64 * S), 0, a.stream, a, nmt);
+    else hipLaunchKernelGGL((qmm_skinny16_kernel<XT, MODE, BITS, S, 2, 4>), grid, dim3(64 * S), 0, a.stream, a, nmt);
+  }
+  return hipGetLastError();
+}
+
+template <int XT, int MODE, int BITS>
+hipError_t s16_launch(const QmmArgs& a) {
+  const int64_t ntiles = (a.N + 15) / 16;
+  const int nmt = (a.M + 31) / 32;
+  const int64_t ny = static_cast<int64_t>(nmt) * a.nbatch;
+  if (ntiles <= 0 || ny <= 0) return hipSuccess;
+  if (ntiles > 0x7fffffffLL || ny > 65535) return hipErrorInvalidConfiguration;
+  const int P = a.K >> 7;
+  const int64_t tiles = ntiles * ny;
+  int S = 2;
+  if (tiles * 2 < 4096 && P >= 16) S = 4;
+  if (tiles * 4 < 4096 && P >= 32) S = 8;
+  static const int tuneS = [] { const char* e = getenv("IQMM_TUNE_SK_S"); return e ? atoi(e) : 0; }();
+  if (tuneS) S = tuneS;
+  const dim3 grid(static_cast<unsigned>(ntiles), static_cast<unsigned>(ny));
+  switch (S) {
+    case 8: return s16_launch_s<XT, MODE, BITS, 8>(a, grid, nmt);
+    case 4: return s16_launch_s<XT, MODE, BITS, 4>(a, grid, nmt);
+    case 1: return s16_launch_s<XT, MODE, BITS, 1>(a, grid, nmt);
+    default: return s16_launch_s<XT, MODE, BITS, 2>(a, grid, nmt);
+  }
+}
+
+template <int XT>
+hipError_t skinny_by_mode(const QmmArgs& a) {
+  static const int tuneF = [] { const char* e = getenv("IQMM_TUNE_SK_F"); return e ? atoi(e) : 2; }();
+  if (tuneF == 2 && a.mode == AFFINE && a.bits == 4 && a.K % 128 == 0) return s16_launch<XT, AFFINE, 4>(a);
+  if (tuneF == 1 && a.mode == AFFINE && a.bits == 4 && a.gs >= 64) return q4f_launch<XT>(a);
+  switch (a.mode) {
+    case AFFINE:
+      switch (a.bits) {
+        case 2: return skinny_launch_t<XT, AFFINE, 2>(a);
+        case 3: return skinny_launch_t<XT, AFFINE, 3>(a);
+        case 4: return skinny_launch_t<XT, AFFINE, 4>(a);
+        case 5: return skinny_launch_t<XT, AFFINE, 5>(a);
+        case 6: return skinny_launch_t<XT, AFFINE, 6>(a);
+        case 8: return skinny_launch_t<XT, AFFINE, 8>(a);
+      }
+      break;
+    case MXFP4: return skinny_launch_t<XT, MXFP4, 4>(a);
+    case MXFP8: return skinny_launch_t<XT, MXFP8, 8>(a);
+    case NVFP4: return skinny_launch_t<XT, NVFP4, 4>(a);
+  }
+  return hipErrorInvalidValue;
+}
+}  // namespace
+
+namespace {
+template <int XT, int MODE, int BITS>
+hipError_t gather_launch_t(const QmmArgs& a, int64_t nflat, int64_t E) {
+  const int64_t ntiles = (a.N + 15) / 16;
+  if (ntiles <= 0 || E <= 0 || nflat <= 0) return hipSuccess;
+  if (E + 1 > 65535 || ntiles > 0x7fffffffLL) return hipErrorInvalidConfiguration;
+  const int P = a.K >> 7;
+  const int S = P >= 8 ? 4 : P >= 4 ? 2 : 1;
+  const dim3 grid(static_cast<unsigned>(ntiles), static_cast<unsigned>(E + 1));
+  switch (S) {
+    case 4: hipLaunchKernelGGL((gather_sorted_kernel<XT, MODE, BITS, 4>), grid, dim3(256), 0, a.stream, a, nflat); break;
+    case 2: hipLaunchKernelGGL((gather_sorted_kernel<XT, MODE, BITS, 2>), grid, dim3(128), 0, a.stream, a, nflat); break;
+    default: hipLaunchKernelGGL((gather_sorted_kernel<XT, MODE, BITS, 1>), grid, dim3(64), 0, a.stream, a, nflat); break;
+  }
+  return hipGetLastError();
+}
+
+template <int XT>
+hipError_t gather_by_mode(const QmmArgs& a, int64_t nflat, int64_t E) {
+  switch (a.mode) {
+    case AFFINE:
+      switch (a.bits) {
+        case 2: return gather_launch_t<XT, AFFINE, 2>(a, nflat, E);
+        case 3: return gather_launch_t<XT, AFFINE, 3>(a, nflat, E);
+        case 4: return gather_launch_t<XT, AFFINE, 4>(a, nflat, E);
+        case 5: return gather_launch_t<XT, AFFINE, 5>(a, nflat, E);
+        case 6: return gather_launch_t<XT, AFFINE, 6>(a, nflat, E);
+        case 8: return gather_launch_t<XT, AFFINE, 8>(a, nflat, E);
+      }
+      break;
+    case MXFP4: return gather_launch_t<XT, MXFP4, 4>(a, nflat, E);
+    case MXFP8: return gather_launch_t<XT, MXFP8, 8>(a, nflat, E);
+    case NVFP4: return gather_launch_t<XT, NVFP4, 4>(a, nflat, E);
+  }
+  return hipErrorInvalidValue;
+}
+}  // namespace
+
+hipError_t launch_gather_sorted(const QmmArgs& a, int64_t nflat, int64_t E) {
+  if (a.xdt == BF16) return gather_by_mode<BF16>(a, nflat, E);
+  if (a.xdt == F16) return gather_by_mode<F16>(a, nflat, E);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_qmm_skinny(const QmmArgs& a) {
+  if (a.xdt == BF16) return skinny_by_mode<BF16>(a);
+  if (a.xdt == F16) return skinny_by_mode<F16>(a);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace iqmm

@@ -281,3 +281,53 @@ def test_gather_qmm_lhs_and_out_of_range(ops):
             ref = oracle.qmm(x[lhs[i]], "f16", w[rhs[i]], s[rhs[i]], b[rhs[i]], "f16", True,
                              32, 4, odt="f32")
             assert rel_err(g[i], ref) <= TOL["f16"]
+
+
+def test_gather_qmm_sorted_with_lhs_and_invalid(ops):
+    """Sorted grouped path: explicit lhs indices, ragged expert counts, an
+    unused expert and an out-of-range expert index (rows of NaN)."""
+    rng = np.random.default_rng(21)
+    E, N, K, M = 6, 48, 256, 1
+    w, s, b = rand_affine(rng, N, K, 64, 4, "bf16", lead=(E,))
+    x = oracle.from_float(rng.standard_normal((7, M, K)).astype(np.float32), "bf16")
+    rhs = np.array([0, 0, 0, 2, 2, 3, 5, 5, 5, 5, 6], np.int32)      # 6 is out of range; 1, 4 unused
+    lhs = np.array([1, 3, 6, 0, 0, 2, 4, 5, 6, 1, 2], np.int32)
+    got = ops.gather_qmm(from_np(x, "bf16"), words_to_torch(w), from_np(s, "bf16"),
+                         from_np(b, "bf16"), torch.from_numpy(lhs).cuda(),
+                         torch.from_numpy(rhs).cuda(), sorted_indices=True)
+    g = as_f64(to_np(got, "bf16"), "bf16")
+    assert g.shape == (11, M, N)
+    for i in range(11):
+        if rhs[i] >= E:
+            assert np.all(np.isnan(g[i]))
+            continue
+        ref = oracle.qmm(x[lhs[i]], "bf16", w[rhs[i]], s[rhs[i]], b[rhs[i]], "bf16", True, 64, 4,
+                         odt="f32")
+        assert rel_err(g[i], ref) <= TOL["bf16"]
+
+
+@pytest.mark.parametrize("mode", ["affine", "nvfp4"])
+def test_gather_qmm_sorted_many_rows_per_expert(ops, mode):
+    """More than 32 rows on one expert exercises the m-tile loop."""
+    rng = np.random.default_rng(22)
+    E, N, K = 3, 40, 512
+    if mode == "affine":
+        w, s, b = rand_affine(rng, N, K, 64, 4, "f16", lead=(E,))
+        ts, tb = from_np(s, "f16"), from_np(b, "f16")
+    else:
+        w, s = rand_fp(rng, N, K, mode, lead=(E,))
+        b = None
+        ts, tb = torch.from_numpy(s).cuda(), None
+    rhs = np.sort(rng.integers(0, E, 90)).astype(np.int64)
+    rhs[:50] = 1
+    rhs = np.sort(rhs)
+    x = oracle.from_float(rng.standard_normal((90, 1, K)).astype(np.float32), "f16")
+    got = ops.gather_qmm(from_np(x, "f16"), words_to_torch(w), ts, tb, None,
+                         torch.from_numpy(rhs).cuda(), mode=mode, sorted_indices=True)
+    g = as_f64(to_np(got, "f16"), "f16")
+    for i in range(90):
+        e = rhs[i]
+        ref = oracle.qmm(x[i], "f16", w[e], s[e], None if b is None else b[e], "f16" if b is not None else None,
+                         True, None if mode != "affine" else 64, None if mode != "affine" else 4, mode,
+                         odt="f32")
+        assert rel_err(g[i], ref) <= (TOL if mode == "affine" else TOL_FP)["f16"]
