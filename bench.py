@@ -52,10 +52,13 @@ def make_weight(ops, N, K, gen, dt=torch.bfloat16, gs=64, bits=4):
 
 
 def time_launches(fn, n, stream):
-    """Average device duration of `fn` over n launches, events bracketing each
-    launch on `stream` (the stream the kernel is enqueued on)."""
+    """Average device duration of `fn` over n launches: HIP events bracket each
+    launch on `stream` (the stream the kernel is enqueued on).  A spin kernel
+    queued first keeps the GPU busy while the host enqueues all n launches,
+    so host-side call overhead never sits between an event pair."""
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(n)]
+    torch.cuda._sleep(int(2.0e6 + 1.5e5 * n))
     for a, b in evs:
         a.record(stream)
         fn()
@@ -128,6 +131,42 @@ def bench_prefill(ops, steps, warmup, M=2048, N=14336, K=4096):
     return {"tflops": flops / avg / 1e12, "avg_launch_us": avg * 1e6, "flops_per_launch": flops}
 
 
+def bench_moe(ops, Ts=(1, 64, 512), reps=10):
+    """Qwen3.5-MoE-style gather_qmm: 256 experts, top-8 of softmax(N(0,1)
+    logits); gate 2048 -> 512 (q4 gs64, bf16).  GB/s counts the bytes of the
+    experts the sampled routing touches (plus x and out)."""
+    E, H, I, k = 256, 2048, 512, 8
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    w = torch.randint(-2**31, 2**31 - 1, (E, I, H // 8), generator=gen, device="cuda",
+                      dtype=torch.int32).view(torch.uint32)
+    s = (torch.rand((E, I, H // 64), generator=gen, device="cuda") * 0.004 + 0.002).to(torch.bfloat16)
+    b = (torch.randn((E, I, H // 64), generator=gen, device="cuda") * 0.02).to(torch.bfloat16)
+    per_expert = I * H // 2 + 2 * I * (H // 64) * 2
+    stream = torch.cuda.current_stream()
+    out = {}
+    for T in Ts:
+        logits = torch.randn((T, E), generator=gen, device="cuda")
+        idx = torch.topk(torch.softmax(logits, -1), k, dim=-1).indices.to(torch.int32)
+        x = torch.randn((T, H), generator=gen, device="cuda").to(torch.bfloat16)
+        uniq = int(torch.unique(idx).numel())
+        if T == 1:
+            xin, rhs, srt = x.view(T, 1, 1, H), idx, False
+        else:
+            flat = idx.view(-1)
+            order = torch.argsort(flat, stable=True)
+            xin, rhs, srt = x[order // k].view(T * k, 1, H).contiguous(), flat[order].contiguous(), True
+        fn = lambda: ops.gather_qmm(xin, w, s, b, None, rhs, True, 64, 4, "affine", srt)  # noqa: E731
+        fn()
+        torch.cuda.synchronize()
+        dt = time_launches(fn, reps, stream)
+        nbytes = uniq * per_expert + T * H * 2 + T * k * I * 2
+        out[str(T)] = {"unique_experts": uniq, "us": round(dt * 1e6, 2),
+                       "gbs": round(nbytes / dt / 1e9, 1),
+                       "tflops": round(2.0 * T * k * I * H / dt / 1e12, 2),
+                       "path": "sorted grouped" if srt else "per-token"}
+    return out
+
+
 def bench_llama_decode(ops, Ms=(1, 4, 8, 16, 32), steps=5):
     """Llama-3-8B-shaped decode step: 32 layers x {q,k,v,o,gate,up,down} of
     distinct 4-bit gs64 weights; tokens/s = M / step time."""
@@ -197,6 +236,29 @@ def cpu_baseline(seconds=10.0, N=14336, K=4096):
                       f"{med * 1e3:.1f} ms) by the oracle's OpenMP streaming qmv"}
 
 
+def run_only(ops, args):
+    """Single-workload mode for profiler passes.  "copy" moves a known number
+    of bytes with a plain device copy, the calibration point for the HBM
+    FETCH_SIZE / WRITE_SIZE counters."""
+    if args.only == "gemv":
+        r = bench_gemv(ops, args.steps, args.warmup)
+        return {"only": "gemv", **{k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()}}
+    if args.only == "prefill":
+        r = bench_prefill(ops, args.steps, args.warmup)
+        return {"only": "prefill", **{k: round(v, 3) for k, v in r.items()}}
+    if args.only == "moe":
+        return {"only": "moe", **bench_moe(ops)}
+    nbytes = 256 << 20
+    a = torch.empty(nbytes // 4, dtype=torch.int32, device="cuda").fill_(1)
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    for _ in range(max(1, args.steps)):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    return {"only": "copy", "bytes_read_per_copy": nbytes, "bytes_written_per_copy": nbytes,
+            "copies": max(1, args.steps)}
+
+
 def load_traffic():
     p = os.path.join(ROOT, "profiles", "traffic.json")
     if os.path.exists(p):
@@ -213,6 +275,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-llama", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--only", choices=["gemv", "prefill", "moe", "copy"], default=None,
+                    help="run one workload (for rocprofv3 kernel-trace / counter passes)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path "
@@ -223,9 +287,14 @@ def main():
     from ironmlx_amd import ops, _lib
     _lib.load()
     torch.cuda.set_device(0)
+    if args.only is not None:
+        print(json.dumps(run_only(ops, args)), flush=True)
+        return
 
     gemv = bench_gemv(ops, args.steps, args.warmup)
     prefill = bench_prefill(ops, args.steps, args.warmup)
+    prefill_down = bench_prefill(ops, args.steps, args.warmup, N=4096, K=14336)
+    moe = bench_moe(ops)
     llama = None if args.no_llama else bench_llama_decode(ops)
     traffic = load_traffic().get("gemv_q4_gs64_k4096_n14336_m1")
     line = {
@@ -257,7 +326,9 @@ def main():
                     "roofline": {"bound": "mfma", "achieved": round(prefill["tflops"], 2),
                                  "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                                  "frac": round(prefill["tflops"] / BF16_PEAK_TFLOPS, 4),
-                                 "avg_launch_us": round(prefill["avg_launch_us"], 2)}},
+                                 "avg_launch_us": round(prefill["avg_launch_us"], 2)},
+                    "down_proj_K14336_N4096_tflops": round(prefill_down["tflops"], 2)},
+        "moe_gather_qmm": moe,
     }
     if llama is not None:
         line["llama3_8b_decode"] = llama

@@ -1,0 +1,74 @@
+"""GPU checks of the caller layer: QuantizedLinear == quantized_matmul,
+QuantizedEmbedding == dequantize + row gather, and MoEMLP (sorted gather_qmm)
+against the reference's per-expert loop restated with quantized_matmul
+(mlx/src/nn/moe.rs:84-170)."""
+import pytest
+import torch
+import torch.nn.functional as F
+
+from ironmlx_amd import nn, ops
+
+pytestmark = pytest.mark.gpu
+
+
+def _q(W, gs=64, bits=4):
+    return ops.quantize(W, gs, bits)
+
+
+def test_quantized_linear_and_embedding():
+    torch.manual_seed(0)
+    W = (torch.randn(96, 256, device="cuda") * 0.02).to(torch.bfloat16)
+    w, s, b = _q(W)
+    lin = nn.QuantizedLinear(w, s, b, 64, 4)
+    x = torch.randn(3, 5, 256, device="cuda").to(torch.bfloat16)
+    assert torch.equal(lin(x), ops.quantized_matmul(x, w, s, b, True, 64, 4, "affine"))
+    emb = nn.QuantizedEmbedding(w, s, b, 64, 4)
+    tok = torch.tensor([[3, 0, 95]], device="cuda")
+    table = ops.dequantize(w, s, b, 64, 4)
+    assert torch.equal(emb(tok), table[tok])
+
+
+def test_moe_matches_per_expert_loop():
+    torch.manual_seed(1)
+    E, H, I, k, T = 16, 256, 128, 4, 37
+    dt = torch.bfloat16
+    def stack(n_out, n_in):
+        W = (torch.randn(E * n_out, n_in, device="cuda") * 0.02).to(dt)
+        w, s, b = _q(W)
+        return w.view(E, n_out, -1), s.view(E, n_out, -1), b.view(E, n_out, -1)
+    gate_up = stack(2 * I, H)
+    down = stack(H, I)
+    p = "layers.0"
+    weights = {f"{p}.mlp.experts.gate_up_proj.weight": gate_up[0],
+               f"{p}.mlp.experts.gate_up_proj.scales": gate_up[1],
+               f"{p}.mlp.experts.gate_up_proj.biases": gate_up[2],
+               f"{p}.mlp.experts.down_proj.weight": down[0],
+               f"{p}.mlp.experts.down_proj.scales": down[1],
+               f"{p}.mlp.experts.down_proj.biases": down[2]}
+    experts = nn.split_fused_experts(weights, p, 64, 4)
+    router = nn.Linear((torch.randn(E, H, device="cuda") * 0.1).to(dt))
+    sh = [nn.QuantizedLinear(*_q((torch.randn(o, i, device="cuda") * 0.02).to(dt)), 64, 4)
+          for (o, i) in [(I, H), (I, H), (H, I)]]
+    shared = nn.MLP(*sh)
+    sgate = nn.Linear((torch.randn(1, H, device="cuda") * 0.1).to(dt))
+    moe = nn.MoEMLP(router, experts, shared, sgate, k, True)
+    x = torch.randn(1, T, H, device="cuda").to(dt)
+    got = moe(x).float()
+
+    # reference: host loop over used experts, one quantized_matmul per projection
+    xf = x.reshape(T, H)
+    scores, idx = moe.route(xf)
+    ref = torch.zeros(T, H, device="cuda")
+    for e in range(E):
+        rows, slots = (idx == e).nonzero(as_tuple=True)
+        if rows.numel() == 0:
+            continue
+        xe = xf[rows]
+        def proj(name, v):
+            st = experts[name]
+            return ops.quantized_matmul(v, st.weight[e], st.scales[e], st.biases[e], True, 64, 4)
+        ye = proj("down", F.silu(proj("gate", xe)) * proj("up", xe))
+        ref.index_add_(0, rows, ye.float() * scores[rows, slots].unsqueeze(-1))
+    ref = ref + (shared(xf).float() * torch.sigmoid(sgate(xf).float()))
+    err = ((got.reshape(T, H) - ref).abs().max() / ref.abs().max()).item()
+    assert err <= 2e-2, err
