@@ -96,13 +96,12 @@ def bench_gemv(ops, steps, warmup, M=1, N=14336, K=4096, pool_bytes=640 << 20):
     t1.record(stream)
     torch.cuda.synchronize()
     total_s = t0.elapsed_time(t1) * 1e-3
-    # per-launch kernel durations, eager, rotating through the pool
-    it = iter(range(10 ** 9))
-    def launch():
-        i = next(it) % P
-        w, s, b = pool[i]
-        ops.quantized_matmul(x, w, s, b, True, 64, 4, "affine")
-    avg_launch_s = time_launches(launch, 4 * P, stream)
+    # The kernel is a few microseconds long, so an event pair around each
+    # launch would time the event records too; the average launch duration is
+    # the timed replays (HIP events on the launch stream) over the launches
+    # they contain.  rocprofv3's kernel trace of `bench.py --only gemv` agrees
+    # (profiles/gemv_q4_gs64_k4096_n14336_m1.md).
+    avg_launch_s = total_s / (steps * P)
     res = {
         "gbs": per * P * steps / total_s / 1e9,
         "ms_per_step": total_s / steps * 1e3,
@@ -296,7 +295,9 @@ def main():
     prefill_down = bench_prefill(ops, args.steps, args.warmup, N=4096, K=14336)
     moe = bench_moe(ops)
     llama = None if args.no_llama else bench_llama_decode(ops)
-    traffic = load_traffic().get("gemv_q4_gs64_k4096_n14336_m1")
+    tr = load_traffic()
+    traffic = tr.get("gemv_q4_gs64_k4096_n14336_m1", {}).get("traffic_bytes")
+    traffic_pf = tr.get("prefill_q4_gs64_m2048_k4096_n14336", {}).get("traffic_bytes")
     line = {
         "metric": "4-bit qmatmul: decode GEMV HBM GB/s (%peak); prefill TFLOP/s (%MFMA peak)",
         "value": round(gemv["gbs"], 1),
@@ -326,7 +327,8 @@ def main():
                     "roofline": {"bound": "mfma", "achieved": round(prefill["tflops"], 2),
                                  "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                                  "frac": round(prefill["tflops"] / BF16_PEAK_TFLOPS, 4),
-                                 "avg_launch_us": round(prefill["avg_launch_us"], 2)},
+                                 "avg_launch_us": round(prefill["avg_launch_us"], 2),
+                                 "traffic": traffic_pf},
                     "down_proj_K14336_N4096_tflops": round(prefill_down["tflops"], 2)},
         "moe_gather_qmm": moe,
     }

@@ -444,14 +444,6 @@ bool qmm_gemm_supported(const QmmArgs& a) {
 }
 
 namespace {
-int gemm_variant() {
-  static const int v = [] {
-    const char* e = getenv("IQMM_TUNE_GEMM");
-    return e ? atoi(e) : 0;
-  }();
-  return v;
-}
-
 template <int XT, int MODE, int BITS>
 hipError_t gemm_launch_t(const QmmArgs& a) {
   const int ntm = (a.M + GBM - 1) / GBM, ntn = (a.N + GBN - 1) / GBN;
@@ -460,8 +452,7 @@ hipError_t gemm_launch_t(const QmmArgs& a) {
   if (nblk > 0x7fffffffLL || a.nbatch > 65535) return hipErrorInvalidConfiguration;
   const dim3 grid(static_cast<unsigned>(nblk), static_cast<unsigned>(a.nbatch));
   const int G = a.K / (MODE == AFFINE ? a.gs : ModeInfo<MODE>::GS);
-  const bool dma_ok = a.transpose && a.K % DBK == 0 && (MODE == AFFINE ? G % 2 == 0 : G % 4 == 0) &&
-                      gemm_variant() != 1;
+  const bool dma_ok = a.transpose && a.K % DBK == 0 && (MODE == AFFINE ? G % 2 == 0 : G % 4 == 0);
   if (dma_ok) {
     auto kern = qmm_gemm_dma_kernel<XT, MODE, BITS>;
     constexpr size_t lds = dma_lds_bytes<BITS, MODE>();

@@ -128,127 +128,6 @@ __global__ __launch_bounds__(64 * S) void qmm_skinny_kernel(QmmArgs a, int nmt) 
 }
 
 // ---------------------------------------------------------------------------
-// Factored variant for affine 4-bit with group_size >= 64 (the common case).
-// In the layout above one 64-code block of a row is exactly one quantization
-// group, so the codes go to the MFMA unconverted: v_perm_b32 against a byte
-// register of 0x43 (bf16) / 0x64 (fp16) turns nibble pairs into the exact
-// 16-bit values C + q (C = 128 / 1024), and per block
-//   acc += s * sum x (C + q)  +  (b - C s) * sum x
-// where sum x over the block comes from one more MFMA chain against ones.
-// x is permuted to the nibble-pair order (n0,n4)(n2,n6)(n1,n5)(n3,n7) of each
-// word.  MT = number of 8-row groups of the 32-row tile that hold rows < M
-// (the epilogue only touches those accumulators).
-template <int XT, int S, int MT>
-__global__ __launch_bounds__(64 * S) void qmm_skinny_q4f_kernel(QmmArgs a, int nmt) {
-  using XS = uint16_t;
-  __shared__ float red[S * 32 * 33];
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int M = a.M, N = a.N, K = a.K;
-  const int n0 = blockIdx.x * SK_ROWS;
-  const int mt = blockIdx.y % nmt;
-  const int64_t bb = blockIdx.y / nmt;
-  const int m0 = mt * 32;
-  XS* out = static_cast<XS*>(a.out) + bb * static_cast<int64_t>(M) * N;
-  int64_t xb = 0, wb = 0;
-  if (a.bm.ndim != 0 || a.bm.lhs != nullptr || a.bm.rhs != nullptr) {
-    if (!map_batch(a.bm, bb, xb, wb)) {
-      for (int i = t; i < 32 * SK_ROWS; i += 64 * S) {
-        const int r = m0 + i / SK_ROWS, c = n0 + i % SK_ROWS;
-        if (r < M && c < N) out[static_cast<int64_t>(r) * N + c] = from_f<XT>(__builtin_nanf(""));
-      }
-      return;
-    }
-  }
-  const XS* x = static_cast<const XS*>(a.x) + xb * a.x_mat;
-  const uint32_t* w = a.w + wb * a.w_mat;
-  const int G = K / a.gs, gshift = __builtin_ctz(a.gs);
-  const XS* sp = static_cast<const XS*>(a.s) + wb * a.s_mat;
-  const XS* bp = static_cast<const XS*>(a.b) + wb * a.s_mat;
-  const int64_t wpr = K >> 3;
-  const int nl = lane & 31, h = lane >> 5;
-  const int row = min(n0 + nl, N - 1);
-  const uint32_t* wrow = w + static_cast<int64_t>(row) * wpr;
-  const XS* srow = sp + static_cast<int64_t>(row) * G;
-  const XS* brow = bp + static_cast<int64_t>(row) * G;
-  const int xm = m0 + nl;
-  const bool xvalid = xm < M;
-  const XS* xrow = x + static_cast<int64_t>(xvalid ? xm : 0) * K;
-  const int P = K >> 6;
-  const int pb = (P * wave) / S, pe = (P * (wave + 1)) / S;
-  constexpr uint32_t E = XT == BF16 ? 0x43434343u : 0x64646464u;
-  constexpr float C = XT == BF16 ? 128.f : 1024.f;
-  constexpr uint32_t ONE2 = XT == BF16 ? 0x3f803f80u : 0x3c003c00u;
-  const g_u32x4_t ones = {ONE2, ONE2, ONE2, ONE2};
-
-  f32x16_t acc;
-#pragma unroll
-  for (int v = 0; v < 16; ++v) acc[v] = 0.f;
-
-  struct Blk {
-    g_u32x4_t wv;
-    XS s, b;
-    g_u32x4_t xa[4];
-  };
-  auto load = [&](int p, Blk& B) {
-    const int pc = min(p, pe - 1);
-    const int c = 2 * pc + h;
-    B.wv = __builtin_nontemporal_load(reinterpret_cast<const g_u32x4_t*>(wrow + c * 4));
-    const int g = (pc << 6) >> gshift;
-    B.s = srow[g];
-    B.b = brow[g];
-    const g_u32x4_t* xp = reinterpret_cast<const g_u32x4_t*>(xrow + c * 32);
-    const bool live = xvalid && p < pe;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) B.xa[j] = live ? xp[j] : g_u32x4_t{0, 0, 0, 0};
-  };
-  auto compute = [&](const Blk& B) {
-    f32x16_t tq, t1;
-#pragma unroll
-    for (int v = 0; v < 16; ++v) { tq[v] = 0.f; t1[v] = 0.f; }
-    const uint32_t wd[4] = {B.wv.x, B.wv.y, B.wv.z, B.wv.w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t lo = wd[j] & 0x0F0F0F0Fu, hi = (wd[j] >> 4) & 0x0F0F0F0Fu;
-      const g_u32x4_t q = {__builtin_amdgcn_perm(E, lo, 0x04020400u),   // n0, n4
-                           __builtin_amdgcn_perm(E, lo, 0x04030401u),   // n2, n6
-                           __builtin_amdgcn_perm(E, hi, 0x04020400u),   // n1, n5
-                           __builtin_amdgcn_perm(E, hi, 0x04030401u)};  // n3, n7
-      const g_u32x4_t xv = B.xa[j];   // x0..x7 as pairs (x0x1)(x2x3)(x4x5)(x6x7)
-      const g_u32x4_t xq = {__builtin_amdgcn_perm(xv.z, xv.x, 0x05040100u),   // x0, x4
-                            __builtin_amdgcn_perm(xv.w, xv.y, 0x05040100u),   // x2, x6
-                            __builtin_amdgcn_perm(xv.z, xv.x, 0x07060302u),   // x1, x5
-                            __builtin_amdgcn_perm(xv.w, xv.y, 0x07060302u)};  // x3, x7
-      tq = mfma32<XT>(xq, q, tq);
-      t1 = mfma32<XT>(xv, ones, t1);
-    }
-    const float s = to_f<XT>(B.s), b = to_f<XT>(B.b);
-    const float bc = fmaf(-C, s, b);
-#pragma unroll
-    for (int v = 0; v < 4 * MT; ++v) acc[v] = fmaf(s, tq[v], fmaf(bc, t1[v], acc[v]));
-  };
-  for (int p = pb; p < pe; p += 2) {
-    Blk B0, B1;
-    load(p, B0);
-    load(p + 1, B1);
-    compute(B0);
-    if (p + 1 < pe) compute(B1);
-  }
-#pragma unroll
-  for (int v = 0; v < 16; ++v) {
-    const int m = 8 * (v >> 2) + 4 * h + (v & 3);
-    red[(wave * 32 + m) * 33 + nl] = acc[v];
-  }
-  __syncthreads();
-  for (int i = t; i < 32 * SK_ROWS; i += 64 * S) {
-    const int m = i / SK_ROWS, n = i % SK_ROWS;
-    float v = 0.f;
-#pragma unroll
-    for (int w2 = 0; w2 < S; ++w2) v += red[(w2 * 32 + m) * 33 + n];
-    if (m0 + m < M && n0 + n < N) out[static_cast<int64_t>(m0 + m) * N + n0 + n] = from_f<XT>(v);
-  }
-}
-
-// ---------------------------------------------------------------------------
 // 16x16x32 variant: lane l = (n = l % 16, q = l / 16) streams chunk 4p + q of
 // row n, so each wave instruction reads 16 rows x 64 contiguous bytes (the
 // 32x32 layout's 32-byte runs leave half-used 128-byte lines behind).  The 32
@@ -574,70 +453,18 @@ hipError_t skinny_launch_t(const QmmArgs& a) {
   int S = 4;
   if (tiles * 4 < 4096 && P >= 32) S = 8;
   if (tiles * 8 < 4096 && P >= 64) S = 16;
-  static const int tuneS = [] { const char* e = getenv("IQMM_TUNE_SK_S"); return e ? atoi(e) : 0; }();
-  static const int tuneU = [] { const char* e = getenv("IQMM_TUNE_SK_U"); return e ? atoi(e) : 0; }();
-  if (tuneS) S = tuneS;
-  const int U = tuneU ? tuneU : 4;
   const dim3 grid(static_cast<unsigned>(ntiles), static_cast<unsigned>(ny));
-#define IQMM_SK(SS, UU) hipLaunchKernelGGL((qmm_skinny_kernel<XT, MODE, BITS, SS, UU>), grid, dim3(64 * SS), 0, a.stream, a, nmt)
-  if (U == 2) {
-    switch (S) { case 16: IQMM_SK(16, 2); break; case 8: IQMM_SK(8, 2); break; default: IQMM_SK(4, 2); break; }
-  } else {
-    switch (S) { case 16: IQMM_SK(16, 4); break; case 8: IQMM_SK(8, 4); break; default: IQMM_SK(4, 4); break; }
-  }
+#define IQMM_SK(SS) hipLaunchKernelGGL((qmm_skinny_kernel<XT, MODE, BITS, SS, 2>), grid, dim3(64 * SS), 0, a.stream, a, nmt)
+  switch (S) { case 16: IQMM_SK(16); break; case 8: IQMM_SK(8); break; default: IQMM_SK(4); break; }
 #undef IQMM_SK
   return hipGetLastError();
-}
-
-template <int XT, int S>
-hipError_t q4f_launch_s(const QmmArgs& a, dim3 grid, int nmt) {
-  // MT: 8-row groups of the 32-row tile that carry rows < M
-  const int rows = a.M >= 32 ? 32 : a.M;
-  const int mtier = rows <= 8 ? 1 : rows <= 16 ? 2 : 4;
-  switch (mtier) {
-    case 1: hipLaunchKernelGGL((qmm_skinny_q4f_kernel<XT, S, 1>), grid, dim3(64 * S), 0, a.stream, a, nmt); break;
-    case 2: hipLaunchKernelGGL((qmm_skinny_q4f_kernel<XT, S, 2>), grid, dim3(64 * S), 0, a.stream, a, nmt); break;
-    default: hipLaunchKernelGGL((qmm_skinny_q4f_kernel<XT, S, 4>), grid, dim3(64 * S), 0, a.stream, a, nmt); break;
-  }
-  return hipGetLastError();
-}
-
-template <int XT>
-hipError_t q4f_launch(const QmmArgs& a) {
-  const int64_t ntiles = (a.N + SK_ROWS - 1) / SK_ROWS;
-  const int nmt = (a.M + 31) / 32;
-  const int64_t ny = static_cast<int64_t>(nmt) * a.nbatch;
-  if (ntiles <= 0 || ny <= 0) return hipSuccess;
-  if (ntiles > 0x7fffffffLL || ny > 65535) return hipErrorInvalidConfiguration;
-  const int P = a.K >> 6;
-  const int64_t tiles = ntiles * ny;
-  int S = 4;
-  if (tiles * 4 < 4096 && P >= 32) S = 8;
-  if (tiles * 8 < 4096 && P >= 64) S = 16;
-  static const int tuneS = [] { const char* e = getenv("IQMM_TUNE_SK_S"); return e ? atoi(e) : 0; }();
-  if (tuneS) S = tuneS;
-  const dim3 grid(static_cast<unsigned>(ntiles), static_cast<unsigned>(ny));
-  switch (S) {
-    case 16: return q4f_launch_s<XT, 16>(a, grid, nmt);
-    case 8: return q4f_launch_s<XT, 8>(a, grid, nmt);
-    default: return q4f_launch_s<XT, 4>(a, grid, nmt);
-  }
 }
 
 template <int XT, int MODE, int BITS, int S>
 hipError_t s16_launch_s(const QmmArgs& a, dim3 grid, int nmt) {
   const int rows = a.M >= 32 ? 32 : a.M;
-  static const int tuneU = [] { const char* e = getenv("IQMM_TUNE_SK_U"); return e ? atoi(e) : 4; }();
-  if (tuneU == 8) {
-    if (rows <= 16) hipLaunchKernelGGL((qmm_skinny16_kernel<XT, MODE, BITS, S, 1, 8>), grid, dim3(64 * S), 0, a.stream, a, nmt);
-    else hipLaunchKernelGGL((qmm_skinny16_kernel<XT, MODE, BITS, S, 2, 8>), grid, dim3(64 * S), 0, a.stream, a, nmt);
-  } else if (tuneU == 2) {
-    if (rows <= 16) hipLaunchKernelGGL((qmm_skinny16_kernel<XT, MODE, BITS, S, 1, 2>), grid, dim3(64 * S), 0, a.stream, a, nmt);
-    else hipLaunchKernelGGL((qmm_skinny16_kernel<XT, MODE, BITS, S, 2, 2>), grid, dim3(64 * S), 0, a.stream, a, nmt);
-  } else {
-    if (rows <= 16) hipLaunchKernelGGL((qmm_skinny16_kernel<XT, MODE, BITS, S, 1, 4>), grid, dim3(64 * S), 0, a.stream, a, nmt);
-    else hipLaunchKernelGGL((qmm_skinny16_kernel<XT, MODE, BITS, S, 2, 4>), grid, dim3(64 * S), 0, a.stream, a, nmt);
-  }
+  if (rows <= 16) hipLaunchKernelGGL((qmm_skinny16_kernel<XT, MODE, BITS, S, 1, 4>), grid, dim3(64 * S), 0, a.stream, a, nmt);
+  else hipLaunchKernelGGL((qmm_skinny16_kernel<XT, MODE, BITS, S, 2, 4>), grid, dim3(64 * S), 0, a.stream, a, nmt);
   return hipGetLastError();
 }
 
@@ -653,22 +480,34 @@ hipError_t s16_launch(const QmmArgs& a) {
   int S = 2;
   if (tiles * 2 < 4096 && P >= 16) S = 4;
   if (tiles * 4 < 4096 && P >= 32) S = 8;
-  static const int tuneS = [] { const char* e = getenv("IQMM_TUNE_SK_S"); return e ? atoi(e) : 0; }();
-  if (tuneS) S = tuneS;
   const dim3 grid(static_cast<unsigned>(ntiles), static_cast<unsigned>(ny));
   switch (S) {
     case 8: return s16_launch_s<XT, MODE, BITS, 8>(a, grid, nmt);
     case 4: return s16_launch_s<XT, MODE, BITS, 4>(a, grid, nmt);
-    case 1: return s16_launch_s<XT, MODE, BITS, 1>(a, grid, nmt);
     default: return s16_launch_s<XT, MODE, BITS, 2>(a, grid, nmt);
   }
 }
 
 template <int XT>
 hipError_t skinny_by_mode(const QmmArgs& a) {
-  static const int tuneF = [] { const char* e = getenv("IQMM_TUNE_SK_F"); return e ? atoi(e) : 2; }();
-  if (tuneF == 2 && a.mode == AFFINE && a.bits == 4 && a.K % 128 == 0) return s16_launch<XT, AFFINE, 4>(a);
-  if (tuneF == 1 && a.mode == AFFINE && a.bits == 4 && a.gs >= 64) return q4f_launch<XT>(a);
+  // 16x16x32 layout (64-byte row runs) when K is a multiple of 128
+  if (a.K % 128 == 0) {
+    switch (a.mode) {
+      case AFFINE:
+        switch (a.bits) {
+          case 2: return s16_launch<XT, AFFINE, 2>(a);
+          case 3: return s16_launch<XT, AFFINE, 3>(a);
+          case 4: return s16_launch<XT, AFFINE, 4>(a);
+          case 5: return s16_launch<XT, AFFINE, 5>(a);
+          case 6: return s16_launch<XT, AFFINE, 6>(a);
+          case 8: return s16_launch<XT, AFFINE, 8>(a);
+        }
+        break;
+      case MXFP4: return s16_launch<XT, MXFP4, 4>(a);
+      case MXFP8: return s16_launch<XT, MXFP8, 8>(a);
+      case NVFP4: return s16_launch<XT, NVFP4, 4>(a);
+    }
+  }
   switch (a.mode) {
     case AFFINE:
       switch (a.bits) {
