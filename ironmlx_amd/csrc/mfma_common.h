@@ -76,4 +76,15 @@ __device__ __forceinline__ void dequant32(const uint32_t (&wd)[BITS], float s, f
   }
 }
 
+// byte k of v as fp32 (v_cvt_f32_ubyte{k})
+template <int B>
+__device__ __forceinline__ float ubyte_f(uint32_t v) {
+  float r;
+  if constexpr (B == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(v));
+  else if constexpr (B == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(v));
+  else if constexpr (B == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(v));
+  else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(v));
+  return r;
+}
+
 }  // namespace iqmm

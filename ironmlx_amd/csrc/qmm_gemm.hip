@@ -27,6 +27,8 @@
 // fastest.
 #include <stdlib.h>
 
+#include <type_traits>
+
 #include "launch.h"
 #include "mfma_common.h"
 
@@ -228,13 +230,14 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
       (const __attribute__((address_space(3))) char*)(p)));
 }
+// lds: wave-uniform LDS byte address (forced into an SGPR for M0)
 __device__ __forceinline__ void dma_x4(const void* g, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
-               :: "v"(g), "s"(lds) : "memory", "m0");
+               :: "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory", "m0");
 }
 __device__ __forceinline__ void dma_x1(const void* g, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
-               :: "v"(g), "s"(lds) : "memory", "m0");
+               :: "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory", "m0");
 }
 
 template <int BITS, int MODE>
@@ -433,6 +436,625 @@ __global__ __launch_bounds__(256, 1) void qmm_gemm_dma_kernel(QmmArgs a, int ntm
     }
 }
 
+// ---------------------------------------------------------------------------
+// Eight-wave DMA kernel: the same pipeline with 512 threads, two waves per
+// SIMD, each wave owning a 64 x 128 sub-tile (2 x 4 blocks of 32 x 32), so one
+// wave's MFMAs overlap the other's dequantization, LDS waits and barrier.
+// DMA instructions are spread round-robin over the waves; each wave waits on
+// its own issue count (wait_vm).
+__device__ __forceinline__ void wait_vm(int n) {
+  switch (n) {
+    case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+    case 1: asm volatile("s_waitcnt vmcnt(1)" ::: "memory"); break;
+    case 2: asm volatile("s_waitcnt vmcnt(2)" ::: "memory"); break;
+    case 3: asm volatile("s_waitcnt vmcnt(3)" ::: "memory"); break;
+    case 4: asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
+    case 5: asm volatile("s_waitcnt vmcnt(5)" ::: "memory"); break;
+    case 6: asm volatile("s_waitcnt vmcnt(6)" ::: "memory"); break;
+    case 7: asm volatile("s_waitcnt vmcnt(7)" ::: "memory"); break;
+    case 8: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
+    case 9: asm volatile("s_waitcnt vmcnt(9)" ::: "memory"); break;
+    case 10: asm volatile("s_waitcnt vmcnt(10)" ::: "memory"); break;
+    case 11: asm volatile("s_waitcnt vmcnt(11)" ::: "memory"); break;
+    case 12: asm volatile("s_waitcnt vmcnt(12)" ::: "memory"); break;
+    case 13: asm volatile("s_waitcnt vmcnt(13)" ::: "memory"); break;
+    case 14: asm volatile("s_waitcnt vmcnt(14)" ::: "memory"); break;
+    case 15: asm volatile("s_waitcnt vmcnt(15)" ::: "memory"); break;
+    case 16: asm volatile("s_waitcnt vmcnt(16)" ::: "memory"); break;
+    case 17: asm volatile("s_waitcnt vmcnt(17)" ::: "memory"); break;
+    case 18: asm volatile("s_waitcnt vmcnt(18)" ::: "memory"); break;
+    case 19: asm volatile("s_waitcnt vmcnt(19)" ::: "memory"); break;
+    case 20: asm volatile("s_waitcnt vmcnt(20)" ::: "memory"); break;
+    case 21: asm volatile("s_waitcnt vmcnt(21)" ::: "memory"); break;
+    case 22: asm volatile("s_waitcnt vmcnt(22)" ::: "memory"); break;
+    case 23: asm volatile("s_waitcnt vmcnt(23)" ::: "memory"); break;
+    case 24: asm volatile("s_waitcnt vmcnt(24)" ::: "memory"); break;
+    case 25: asm volatile("s_waitcnt vmcnt(25)" ::: "memory"); break;
+    case 26: asm volatile("s_waitcnt vmcnt(26)" ::: "memory"); break;
+    case 27: asm volatile("s_waitcnt vmcnt(27)" ::: "memory"); break;
+    case 28: asm volatile("s_waitcnt vmcnt(28)" ::: "memory"); break;
+    case 29: asm volatile("s_waitcnt vmcnt(29)" ::: "memory"); break;
+    case 30: asm volatile("s_waitcnt vmcnt(30)" ::: "memory"); break;
+    default: asm volatile("s_waitcnt vmcnt(31)" ::: "memory"); break;
+  }
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmc() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <int I, int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
+}
+
+template <int XT, int MODE, int BITS>
+__global__ __launch_bounds__(512, 1) void qmm_gemm_dma8_kernel(QmmArgs a, int ntm, int ntn) {
+  using XS = uint16_t;
+  using DC = DmaCounts<BITS, MODE>;
+  constexpr bool AFF = MODE == AFFINE;
+  constexpr int NW = 8;
+  constexpr int WINSTR = 4 * BITS;   // dword DMA instructions for the packed W stage
+  extern __shared__ __attribute__((aligned(16))) uint16_t glds[];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6, wm = wave >> 1, wn = wave & 1;
+  const int M = a.M, N = a.N, K = a.K;
+  const int nblk = ntm * ntn;
+  int bid = blockIdx.x;
+  if ((nblk & 7) == 0) bid = (bid & 7) * (nblk >> 3) + (bid >> 3);
+  const int tm = bid % ntm, tn = bid / ntm;
+  const int m0 = tm * GBM, n0 = tn * GBN;
+  const int64_t bb = blockIdx.y;
+  XS* out = static_cast<XS*>(a.out) + bb * static_cast<int64_t>(M) * N;
+  int64_t xb = 0, wb = 0;
+  if (a.bm.ndim != 0 || a.bm.lhs != nullptr || a.bm.rhs != nullptr) {
+    if (!map_batch(a.bm, bb, xb, wb)) {
+      for (int i = t; i < GBM * GBN; i += 512) {
+        const int r = m0 + i / GBN, c = n0 + i % GBN;
+        if (r < M && c < N) out[static_cast<int64_t>(r) * N + c] = from_f<XT>(__builtin_nanf(""));
+      }
+      return;
+    }
+  }
+  const XS* x = static_cast<const XS*>(a.x) + xb * a.x_mat;
+  const uint32_t* w = a.w + wb * a.w_mat;
+  const int gs = AFF ? a.gs : ModeInfo<MODE>::GS;
+  const int G = K / gs;
+  const int64_t wpr = static_cast<int64_t>(K) * BITS / 32;
+  const char* sbase = static_cast<const char*>(a.s) + wb * a.s_mat * (AFF ? 2 : 1);
+  const char* bbase = AFF ? static_cast<const char*>(a.b) + wb * a.s_mat * 2 : nullptr;
+
+  // LDS map (bytes from glds): x ring | W-packed ring | scale ring | bias ring | deq-W ring
+  constexpr int XR = 0;
+  constexpr int WR = XR + DEPTH * DA_STAGE * 2;
+  constexpr int SR = WR + DEPTH * DC::WBYTES;
+  constexpr int BR = SR + DEPTH * GBN * 4;
+  constexpr int DQ = BR + DEPTH * GBN * 4;
+  char* lb = reinterpret_cast<char*>(glds);
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(lb));
+
+  // ---- per-lane DMA sources at k0 = 0 (advanced by k0 each step)
+  const XS* xsrc[2];
+  uint32_t xdst[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int rbase = (wave + NW * i) * 16;
+    const int row = rbase + (lane >> 2);
+    const int g = ((lane & 3) ^ dswzf(row)) & 3;
+    xsrc[i] = x + static_cast<int64_t>(min(m0 + row, M - 1)) * K + g * 8;
+    xdst[i] = rbase * DBK * 2;
+  }
+  const int my_w = (WINSTR - wave + NW - 1) / NW;
+  const int my_s = AFF ? 1 : (wave < 4 ? 1 : 0);
+  const int per_step = 2 + my_w + my_s;
+  const int gshift = __builtin_ctz(gs);
+  // wave-uniform LDS destinations (SGPRs) and per-lane sources at k0 = 0
+  uint32_t xdst_s[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) xdst_s[i] = __builtin_amdgcn_readfirstlane(lds0 + XR + xdst[i]);
+  constexpr int MAXW = (WINSTR + NW - 1) / NW;
+  const uint32_t* wsrc[MAXW];
+  uint32_t wdst_s[MAXW];
+#pragma unroll
+  for (int jj = 0; jj < MAXW; ++jj) {
+    const int j = min(wave + NW * jj, WINSTR - 1);
+    const int idx = j * 64 + lane;
+    const int row = idx / BITS, word = idx - row * BITS;
+    wsrc[jj] = w + min(n0 + row, N - 1) * wpr + word;
+    wdst_s[jj] = __builtin_amdgcn_readfirstlane(lds0 + WR + j * 256);
+  }
+  const int srow = min(n0 + (wave & 3) * 64 + lane, N - 1);
+  const char* ssrc = ((AFF && wave >= 4) ? bbase : sbase) + static_cast<int64_t>(srow) * G * (AFF ? 2 : 1);
+  const uint32_t sdst_s = __builtin_amdgcn_readfirstlane(lds0 + (AFF && wave >= 4 ? BR : SR) + (wave & 3) * 256);
+
+  auto issue = [&](int ks, auto slot_c) {
+    constexpr int SL = decltype(slot_c)::value;
+    const int k0 = ks * DBK;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) dma_x4(xsrc[i] + k0, xdst_s[i] + SL * DA_STAGE * 2);
+#pragma unroll
+    for (int jj = 0; jj < MAXW; ++jj)
+      if (jj < my_w) dma_x1(wsrc[jj] + (k0 >> 5) * BITS, wdst_s[jj] + SL * DC::WBYTES);
+    if (my_s) {
+      const int g = k0 >> gshift;
+      const int ge = AFF ? (g & ~1) : (g & ~3);
+      dma_x1(ssrc + ge * (AFF ? 2 : 1), sdst_s + SL * GBN * 4);
+    }
+  };
+
+  // thread t dequantizes codes [16 h, 16 h + 16) of W row t / 2 (h = t & 1)
+  const int dn = t >> 1, dh = t & 1;
+  int dqoff[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) dqoff[i] = dswz(dn, 16 * dh + 8 * i) * 2;
+  auto dequant = [&](int ks, auto slot_c, auto dst_c) {
+    constexpr int SL = decltype(slot_c)::value, DS = decltype(dst_c)::value;
+    const int k0 = ks * DBK;
+    const uint32_t* wp = reinterpret_cast<const uint32_t*>(lb + WR + SL * DC::WBYTES) + dn * BITS;
+    const int g = k0 >> gshift;
+    const uint32_t sw = reinterpret_cast<const uint32_t*>(lb + SR + SL * GBN * 4)[dn];
+    float sv, bv = 0.f;
+    if constexpr (AFF) {
+      const uint32_t bw = reinterpret_cast<const uint32_t*>(lb + BR + SL * GBN * 4)[dn];
+      sv = to_f<XT>(static_cast<uint16_t>((g & 1) ? (sw >> 16) : (sw & 0xffffu)));
+      bv = to_f<XT>(static_cast<uint16_t>((g & 1) ? (bw >> 16) : (bw & 0xffffu)));
+    } else {
+      const int gg = MODE == NVFP4 ? g + dh : g;
+      sv = fp_scale<MODE>((sw >> (8 * (gg & 3))) & 0xffu);
+    }
+    uint32_t o[8];
+    if constexpr (AFF && BITS == 4) {
+      const uint2 wd2 = *reinterpret_cast<const uint2*>(wp + 2 * dh);
+      const uint32_t wdq[2] = {wd2.x, wd2.y};
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const uint32_t lo = wdq[q] & 0x0F0F0F0Fu, hi = (wdq[q] >> 4) & 0x0F0F0F0Fu;
+        o[4 * q + 0] = pack2<XT>(fmaf(sv, ubyte_f<0>(lo), bv), fmaf(sv, ubyte_f<0>(hi), bv));
+        o[4 * q + 1] = pack2<XT>(fmaf(sv, ubyte_f<1>(lo), bv), fmaf(sv, ubyte_f<1>(hi), bv));
+        o[4 * q + 2] = pack2<XT>(fmaf(sv, ubyte_f<2>(lo), bv), fmaf(sv, ubyte_f<2>(hi), bv));
+        o[4 * q + 3] = pack2<XT>(fmaf(sv, ubyte_f<3>(lo), bv), fmaf(sv, ubyte_f<3>(hi), bv));
+      }
+    } else {
+      uint32_t wd[BITS];
+#pragma unroll
+      for (int i = 0; i < BITS; ++i) wd[i] = wp[i];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float v[2];
+#pragma unroll
+        for (int e2 = 0; e2 < 2; ++e2) {
+          const uint32_t qc = chunk_code<BITS>(wd, 16 * dh + 2 * i + e2);
+          if constexpr (AFF) v[e2] = fmaf(sv, static_cast<float>(qc), bv);
+          else v[e2] = fp_elem<MODE>(qc) * sv;
+        }
+        o[i] = pack2<XT>(v[0], v[1]);
+      }
+    }
+    char* B = lb + DQ + DS * DB_STAGE * 2;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      *reinterpret_cast<g_u32x4_t*>(B + dqoff[i]) = g_u32x4_t{o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]};
+  };
+
+  // fragment offsets (bytes within a stage) for both 16-k halves of a step
+  int offA[2][2], offB[2][4];
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) {
+    const int kq = kk * 16 + 8 * (lane >> 5);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) offA[kk][i] = dswz(wm * 64 + i * 32 + (lane & 31), kq) * 2;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) offB[kk][j] = dswz(wn * 128 + j * 32 + (lane & 31), kq) * 2;
+  }
+
+  f32x16_t acc[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  auto mfma_step = [&](auto sa_c, auto sb_c) {
+    constexpr int SA = decltype(sa_c)::value, SB = decltype(sb_c)::value;
+    const char* Ast = lb + XR + SA * DA_STAGE * 2;
+    const char* Bst = lb + DQ + SB * DB_STAGE * 2;
+    g_u32x4_t af[2][2], bf[2][4];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) af[kk][i] = *reinterpret_cast<const g_u32x4_t*>(Ast + offA[kk][i]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bf[kk][j] = *reinterpret_cast<const g_u32x4_t*>(Bst + offB[kk][j]);
+    }
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma32<XT>(af[kk][i], bf[kk][j], acc[i][j]);
+  };
+
+  const int nk = K / DBK;
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
+  if (nk > 0) issue(0, I0{});
+  if (nk > 1) issue(1, I1{});
+  if (nk > 2) issue(2, I2{});
+  asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+  dequant(0, I0{}, I0{});
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+  // one K step: DMA step ks+3 into slot (ks+3)%4, MFMA on slot ks%4 / deq ks%2,
+  // dequantize step ks+1 (slot (ks+1)%4) into deq (ks+1)%2
+  auto step = [&](int ks, auto sa_c, auto sdq_c, auto snext_c, auto sissue_c) {
+    const bool pre = ks + DEPTH - 1 < nk;
+    if (pre) issue(ks + DEPTH - 1, sissue_c);
+    mfma_step(sa_c, sdq_c);
+    if (ks + 1 < nk) dequant(ks + 1, snext_c, std::integral_constant<int, 1 - decltype(sdq_c)::value>{});
+    __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);
+#pragma unroll
+    for (int g = 0; g < 16; ++g) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+      if (g % 4 == 3) __builtin_amdgcn_sched_group_barrier(0x300, 2, 0);
+    }
+    if (ks + 2 < nk && pre) wait_vm(per_step);
+    else wait_vm(0);
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  };
+  for (int ks = 0; ks < nk; ks += 4) {
+    step(ks, I0{}, I0{}, I1{}, I3{});
+    if (ks + 1 < nk) step(ks + 1, I1{}, I1{}, I2{}, I0{});
+    if (ks + 2 < nk) step(ks + 2, I2{}, I0{}, I3{}, I1{});
+    if (ks + 3 < nk) step(ks + 3, I3{}, I1{}, I0{}, I2{});
+  }
+
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int col = n0 + wn * 128 + j * 32 + (lane & 31);
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int row = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+        if (row < M && col < N) out[static_cast<int64_t>(row) * N + col] = from_f<XT>(acc[i][j][v]);
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Register-B kernel (4- and 8-bit codes).  Wave w owns the 256 x 32 column
+// strip [32 w, 32 w + 32) of the tile, so its B operand is private: each lane
+// dequantizes its two 32x32x16 B fragments straight from the packed ring into
+// registers one step ahead of the MFMAs, and x is the only operand read from
+// LDS per MFMA.
+//
+// Loads are sized by cache-line requests, which bound the DMA rate: x comes
+// per step (256 rows x 64 B), packed W in chunks of WC steps (64 B per row:
+// 4 steps at 4 bits, 2 at 8 bits) and scales / biases in chunks of 16 bytes
+// per row (8 bf16/fp16 groups, or 16 one-byte MX / NV groups), all as
+// 16-byte-per-lane DMAs.  The k order inside a step is permuted identically
+// for both operands: lane half h of fragment kk covers k = 16 h + 8 kk .. +8,
+// which is packed word 2 h + kk at 4 bits, so a lane's B codes are one
+// contiguous 8- or 16-byte read.
+template <int BITS>
+struct WrCfg {
+  static constexpr int STEP_B = 4 * BITS;          // packed bytes per row per step
+  static constexpr int WC = 64 / STEP_B;           // steps per W chunk
+  static constexpr int WSLOT = GBN * 64;           // bytes per W chunk slot
+  // chunk slots: a slot is refilled WD-1 = 5 steps before its chunk starts,
+  // which must come after the last read of the chunk it held: (WSL-1) WC > 3
+  static constexpr int WSL = BITS == 4 ? 2 : 3;
+};
+
+template <int XT, int MODE, int BITS, int WD, int NCB, int ABL = 0>
+__global__ __launch_bounds__(512 / NCB, 1) void qmm_gemm_wr_kernel(QmmArgs a, int ntm, int ntn) {
+  static_assert(BITS == 4 || BITS == 8, "register-B kernel takes 4- and 8-bit codes");
+  static_assert(WD % 2 == 0 && WD >= 6, "B double buffer alternates with the x slot");
+  using XS = uint16_t;
+  using CF = WrCfg<BITS>;
+  constexpr bool AFF = MODE == AFFINE;
+  constexpr int NW = 8 / NCB;          // waves; wave w owns columns [32 NCB w, 32 NCB (w + 1))
+  constexpr int NT = 64 * NW;
+  constexpr int XI = 16 / NW;           // x / W-chunk DMA instructions per wave
+  constexpr int SI = AFF ? 8 / NW : (NW >= 4 ? 1 : 4 / NW);  // scale-chunk instructions (waves < SW)
+  constexpr int SW = AFF ? NW : (NW >= 4 ? 4 : NW);
+  constexpr int GPC = AFF ? 8 : 16;  // groups per 16-byte scale chunk row
+  extern __shared__ __attribute__((aligned(16))) uint16_t glds[];
+  const int t = threadIdx.x, lane = t & 63, h = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);  // uniform: keeps DMA counts scalar
+  const int M = a.M, N = a.N, K = a.K;
+  const int nblk = ntm * ntn;
+  int bid = blockIdx.x;
+  if ((nblk & 7) == 0) bid = (bid & 7) * (nblk >> 3) + (bid >> 3);
+  const int tm = bid % ntm, tn = bid / ntm;
+  const int m0 = tm * GBM, n0 = tn * GBN;
+  const int64_t bb = blockIdx.y;
+  XS* out = static_cast<XS*>(a.out) + bb * static_cast<int64_t>(M) * N;
+  int64_t xb = 0, wb = 0;
+  if (a.bm.ndim != 0 || a.bm.lhs != nullptr || a.bm.rhs != nullptr) {
+    if (!map_batch(a.bm, bb, xb, wb)) {
+      for (int i = t; i < GBM * GBN; i += NT) {
+        const int r = m0 + i / GBN, c = n0 + i % GBN;
+        if (r < M && c < N) out[static_cast<int64_t>(r) * N + c] = from_f<XT>(__builtin_nanf(""));
+      }
+      return;
+    }
+  }
+  const XS* x = static_cast<const XS*>(a.x) + xb * a.x_mat;
+  const char* w = reinterpret_cast<const char*>(a.w + wb * a.w_mat);
+  const int gs = AFF ? a.gs : ModeInfo<MODE>::GS;
+  const int G = K / gs;
+  const int64_t wrow = static_cast<int64_t>(K) * BITS / 8;   // packed bytes per W row
+  const int ssz = AFF ? 2 : 1;                               // bytes per scale
+  const char* sbase = static_cast<const char*>(a.s) + wb * a.s_mat * ssz;
+  const char* bbase = AFF ? static_cast<const char*>(a.b) + wb * a.s_mat * 2 : nullptr;
+
+  // LDS map (bytes from glds): x ring (WD) | W chunk ring (WSL) | scale ring (2) | bias ring (2)
+  constexpr int XR = 0;
+  constexpr int WR = XR + WD * DA_STAGE * 2;
+  constexpr int SR = WR + CF::WSL * CF::WSLOT;
+  constexpr int SSLOT = GBN * 16;
+  constexpr int BR = SR + 2 * SSLOT;
+  char* lb = reinterpret_cast<char*>(glds);
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(lb));
+
+  // ---- DMA sources at k = 0 and wave-uniform destinations
+  const XS* xsrc[XI];
+  uint32_t xdst_s[XI];
+#pragma unroll
+  for (int i = 0; i < XI; ++i) {
+    const int rbase = (wave + NW * i) * 16;
+    const int row = rbase + (lane >> 2);
+    const int g = ((lane & 3) ^ dswzf(row)) & 3;
+    xsrc[i] = x + static_cast<int64_t>(min(m0 + row, M - 1)) * K + g * 8;
+    xdst_s[i] = __builtin_amdgcn_readfirstlane(lds0 + XR + rbase * DBK * 2);
+  }
+  // W chunk: 256 rows x 4 granules = 16 instructions; stored granule p of
+  // row r holds logical granule p ^ f(r)
+  const char* wsrc[XI];
+  uint32_t wdst_s[XI];
+#pragma unroll
+  for (int i = 0; i < XI; ++i) {
+    const int j = wave + NW * i;
+    const int row = j * 16 + (lane >> 2);
+    const int g = ((lane & 3) ^ dswzf(row)) & 3;
+    wsrc[i] = w + static_cast<int64_t>(min(n0 + row, N - 1)) * wrow + g * 16;
+    wdst_s[i] = __builtin_amdgcn_readfirstlane(lds0 + WR + j * 1024);
+  }
+  // scale chunk: 64 rows x 16 B per instruction; 4 instructions of scales
+  // (+ 4 of biases), instruction q = wave + NW i on waves < SW
+  const int my_s = wave < SW ? SI : 0;
+  const char* ssrc[SI];
+  uint32_t sdst_s[SI];
+#pragma unroll
+  for (int i = 0; i < SI; ++i) {
+    const int q = min(wave + NW * i, AFF ? 7 : 3);
+    const int srow = min(n0 + (q & 3) * 64 + lane, N - 1);
+    ssrc[i] = ((AFF && q >= 4) ? bbase : sbase) + static_cast<int64_t>(srow) * G * ssz;
+    sdst_s[i] = __builtin_amdgcn_readfirstlane(lds0 + (AFF && q >= 4 ? BR : SR) + (q & 3) * 1024);
+  }
+  const int gshift = __builtin_ctz(gs);
+  // steps per scale chunk (P = GPC * gs / 32 >= 8)
+  const int pshift = __builtin_ctz(GPC) + gshift - 5;
+  constexpr int WCS = BITS == 4 ? 2 : 1;  // log2(WC)
+
+  // DMAs for step j into x slot SL; W chunk when j % WC == 0 (compile-time
+  // in the unrolled loop), scale chunk when j % P == 0
+  auto issue = [&](int j, auto slot_c, auto wchunk_c) {
+    constexpr int SL = decltype(slot_c)::value;
+    constexpr bool WCH = decltype(wchunk_c)::value;
+    const int k0 = (ABL & 2) ? 0 : j * DBK;
+    if (ABL & 8) return;
+#pragma unroll
+    for (int i = 0; i < XI; ++i) dma_x4(xsrc[i] + k0, xdst_s[i] + SL * DA_STAGE * 2);
+    if constexpr (WCH) {
+      const uint32_t wsl = ((j >> WCS) % CF::WSL) * CF::WSLOT;
+#pragma unroll
+      for (int i = 0; i < XI; ++i) dma_x4(wsrc[i] + (k0 >> 5) * CF::STEP_B, wdst_s[i] + wsl);
+    }
+    if ((j & ((1 << pshift) - 1)) == 0 && my_s) {
+      const int g0 = k0 >> gshift;
+#pragma unroll
+      for (int i = 0; i < SI; ++i) dma_x4(ssrc[i] + g0 * ssz, sdst_s[i] + ((j >> pshift) & 1) * SSLOT);
+    }
+  };
+
+  // ---- B fragments of step ks for column cn of the tile
+  auto deq_b = [&](int ks, int cb, g_u32x4_t (&bo)[2]) {
+    const int cn = 32 * (NCB * wave + cb) + (lane & 31);
+    const int wsw = dswzf(cn);
+    const int g = (ks * DBK) >> gshift;
+    const char* ch = lb + WR + ((ks >> WCS) % CF::WSL) * CF::WSLOT;
+    const char* sc = lb + ((ks >> pshift) & 1) * SSLOT + cn * 16;
+    const int gi = g & (GPC - 1);
+    float sv[2], bv = 0.f;
+    if constexpr (AFF) {
+      sv[0] = sv[1] = to_f<XT>(*reinterpret_cast<const uint16_t*>(sc + SR + gi * 2));
+      bv = to_f<XT>(*reinterpret_cast<const uint16_t*>(sc + BR + gi * 2));
+    } else {
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        // nvfp4: 16-wide groups; fragment kk of half h covers k 16 h + 8 kk
+        const int gg = MODE == NVFP4 ? gi + h : gi;
+        sv[kk] = fp_scale<MODE>(*reinterpret_cast<const uint8_t*>(sc + SR + gg));
+      }
+    }
+    uint32_t wv[4];
+    if constexpr (BITS == 4) {
+      const int gr = (ks & 3) ^ wsw;
+      const uint2 d = *reinterpret_cast<const uint2*>(ch + cn * 64 + gr * 16 + 8 * h);
+      wv[0] = d.x; wv[1] = d.y;
+    } else {
+      const int gr = ((2 * (ks & 1) + h) ^ wsw) & 3;
+      const g_u32x4_t d = *reinterpret_cast<const g_u32x4_t*>(ch + cn * 64 + gr * 16);
+      wv[0] = d[0]; wv[1] = d[1]; wv[2] = d[2]; wv[3] = d[3];
+    }
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      uint32_t o[4];
+      if constexpr (BITS == 4) {
+        const uint32_t lo = wv[kk] & 0x0F0F0F0Fu, hi = (wv[kk] >> 4) & 0x0F0F0F0Fu;
+        if constexpr (AFF) {
+          o[0] = pack2<XT>(fmaf(sv[kk], ubyte_f<0>(lo), bv), fmaf(sv[kk], ubyte_f<0>(hi), bv));
+          o[1] = pack2<XT>(fmaf(sv[kk], ubyte_f<1>(lo), bv), fmaf(sv[kk], ubyte_f<1>(hi), bv));
+          o[2] = pack2<XT>(fmaf(sv[kk], ubyte_f<2>(lo), bv), fmaf(sv[kk], ubyte_f<2>(hi), bv));
+          o[3] = pack2<XT>(fmaf(sv[kk], ubyte_f<3>(lo), bv), fmaf(sv[kk], ubyte_f<3>(hi), bv));
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            o[e] = pack2<XT>(fp_elem<MODE>((lo >> (8 * e)) & 0xfu) * sv[kk],
+                             fp_elem<MODE>((hi >> (8 * e)) & 0xfu) * sv[kk]);
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t d = wv[2 * kk + (e >> 1)] >> (16 * (e & 1));
+          if constexpr (AFF)
+            o[e] = pack2<XT>(fmaf(sv[kk], static_cast<float>(d & 0xffu), bv),
+                             fmaf(sv[kk], static_cast<float>((d >> 8) & 0xffu), bv));
+          else
+            o[e] = pack2<XT>(fp_elem<MODE>(d & 0xffu) * sv[kk], fp_elem<MODE>((d >> 8) & 0xffu) * sv[kk]);
+        }
+      }
+      bo[kk] = g_u32x4_t{o[0], o[1], o[2], o[3]};
+    }
+  };
+
+  // A fragment (kk, block i): rows 32 i + lane % 32, k = 16 h + 8 kk; the
+  // swizzle depends on row % 32 only, so block i is +i * 32 rows.
+  int offA[2];
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) offA[kk] = dswz(lane & 31, 16 * h + 8 * kk) * 2;
+
+  f32x16_t acc[8][NCB];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int c = 0; c < NCB; ++c)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][c][v] = 0.f;
+
+  // MFMAs of one step; each A fragment register is refilled with the next
+  // step's fragment (slot sn, resident since the previous barrier) right after
+  // its last use, so the next step starts with its operands in flight.
+  auto mfma_step = [&](const g_u32x4_t (&bf)[NCB][2], g_u32x4_t (&af)[2][8], auto sn_c) {
+    constexpr int SN = decltype(sn_c)::value;
+    const char* An = lb + XR + SN * DA_STAGE * 2;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+#pragma unroll
+        for (int c = 0; c < NCB; ++c) acc[i][c] = mfma32<XT>(af[kk][i], bf[c][kk], acc[i][c]);
+        af[kk][i] = *reinterpret_cast<const g_u32x4_t*>(An + offA[kk] + i * 32 * DBK * 2);
+      }
+  };
+
+  // x ring of WD stages: step ks lives in slot ks % WD; DMAs run WD-1 steps
+  // ahead.  Step ks dequantizes step ks+1's B and reads step ks+1's A, so the
+  // wait closing step ks must leave steps ks+1 and ks+2 resident: only the
+  // DMAs of steps ks+3 .. ks+WD-1 may still be in flight.  W / scale chunk
+  // slots are refilled only after every reader of their previous chunk has
+  // passed a barrier ((WSL - 1) WC > WD - 3 and P > WD - 3 steps).
+  const int nk = K / DBK;
+  g_u32x4_t bq[2][NCB][2], af[2][8];
+  static_for<0, WD - 1>([&](auto s_c) {
+    constexpr int J = decltype(s_c)::value;
+    if (J < nk) issue(J, s_c, std::integral_constant<bool, J % CF::WC == 0>{});
+  });
+  // steps 0 and 1 resident: DMAs of steps 2 .. WD-2 may stay in flight
+  if (!(ABL & 8)) {
+    if (nk >= WD - 1) {
+      constexpr int nx = [] {
+        int n = 0;
+        for (int j = 2; j <= WD - 2; ++j) n += XI + (j % CF::WC == 0 ? XI : 0);
+        return n;
+      }();
+      wait_vmc<nx>();   // scale chunks are issued at j = 0 only within 0 .. WD-2 (P >= 8)
+    } else {
+      wait_vmc<0>();
+    }
+  }
+  asm volatile("s_barrier" ::: "memory");
+#pragma unroll
+  for (int c = 0; c < NCB; ++c) deq_b(0, c, bq[0][c]);
+  {
+    const char* Ast = lb + XR;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        af[kk][i] = *reinterpret_cast<const g_u32x4_t*>(Ast + offA[kk] + i * 32 * DBK * 2);
+  }
+
+  // unrolled by U = lcm(WD, WC) so the x slot, the B buffer and the W-chunk
+  // issue pattern are compile-time; steady-state waits are immediates.
+  constexpr int U = WD % CF::WC == 0 ? WD : WD * CF::WC / (WD % CF::WC == 2 ? 2 : 1);
+  static_assert(U % WD == 0 && U % CF::WC == 0, "unroll must cover both periods");
+  const int pmask = (1 << pshift) - 1;
+  for (int ks0 = 0; ks0 < nk; ks0 += U) {
+    static_for<0, U>([&](auto s_c) {
+      constexpr int S = decltype(s_c)::value;
+      const int ks = ks0 + S;
+      if (ks < nk) {
+        const bool steady = ks + WD - 1 < nk;
+        if (steady)
+          issue(ks + WD - 1, std::integral_constant<int, (S + WD - 1) % WD>{},
+                std::integral_constant<bool, (S + WD - 1) % CF::WC == 0>{});
+        if (!(ABL & 4)) {
+#pragma unroll
+          for (int c = 0; c < NCB; ++c) deq_b(ks + 1, c, bq[(S + 1) & 1][c]);
+        }
+        if (!(ABL & 1)) mfma_step(bq[S & 1], af, std::integral_constant<int, (S + 1) % WD>{});
+        if (!(ABL & 8)) {
+          if (steady) {
+            // DMAs of steps ks+3 .. ks+WD-1 may stay in flight
+            constexpr int nx = [] {
+              int n = 0;
+              for (int j = S + 3; j <= S + WD - 1; ++j) n += XI + (j % CF::WC == 0 ? XI : 0);
+              return n;
+            }();
+            if (my_s && ((ks + WD - 1) & pmask) <= WD - 4) wait_vmc<nx + SI>();
+            else wait_vmc<nx>();
+          } else {
+            wait_vmc<0>();  // last WD-1 steps: nothing further is issued
+          }
+        }
+        // the A reads still in flight target slot ks+1, which no DMA issued
+        // before the next barrier touches, so the barrier need not drain them
+        asm volatile("s_barrier" ::: "memory");
+      }
+    });
+  }
+
+#pragma unroll
+  for (int c = 0; c < NCB; ++c) {
+    const int col = n0 + 32 * (NCB * wave + c) + (lane & 31);
+    if (col < N) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int row = m0 + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+          if (row < M) out[static_cast<int64_t>(row) * N + col] = from_f<XT>(acc[i][c][v]);
+        }
+    }
+  }
+}
+
+template <int BITS>
+constexpr size_t wr_lds_bytes(int wd) {
+  return static_cast<size_t>(wd) * DA_STAGE * 2 + WrCfg<BITS>::WSL * WrCfg<BITS>::WSLOT + 4 * GBN * 16;
+}
+
 template <int BITS, int MODE>
 constexpr size_t dma_lds_bytes() {
   return DEPTH * DA_STAGE * 2 + DEPTH * DmaCounts<BITS, MODE>::WBYTES + 2 * DEPTH * GBN * 4 +
@@ -453,7 +1075,39 @@ hipError_t gemm_launch_t(const QmmArgs& a) {
   const dim3 grid(static_cast<unsigned>(nblk), static_cast<unsigned>(a.nbatch));
   const int G = a.K / (MODE == AFFINE ? a.gs : ModeInfo<MODE>::GS);
   const bool dma_ok = a.transpose && a.K % DBK == 0 && (MODE == AFFINE ? G % 2 == 0 : G % 4 == 0);
-  if (dma_ok) {
+  static const int v8 = [] { const char* e = getenv("IQMM_TUNE_GEMM8"); return e ? atoi(e) : 2; }();
+  static const int abl = [] { const char* e = getenv("IQMM_ABL"); return e ? atoi(e) : 0; }();
+  constexpr int WD = 6;
+  constexpr int GPC = MODE == AFFINE ? 8 : 16;
+  const bool wr_ok = dma_ok && (BITS == 4 || BITS == 8) && a.K % (32 * (BITS == 4 ? 4 : 2)) == 0 &&
+                     G % GPC == 0;
+  if (wr_ok && v8 == 2) {
+    if constexpr (BITS == 4 || BITS == 8) {
+      auto kern = qmm_gemm_wr_kernel<XT, MODE, BITS, WD, 1>;
+      int nt = 512;
+      if constexpr (XT == BF16 && MODE == AFFINE && BITS == 4) {
+        switch (abl) {
+          case 1: kern = qmm_gemm_wr_kernel<XT, MODE, BITS, WD, 1, 1>; break;
+          case 8: kern = qmm_gemm_wr_kernel<XT, MODE, BITS, WD, 1, 8>; break;
+          case 12: kern = qmm_gemm_wr_kernel<XT, MODE, BITS, WD, 1, 12>; break;
+          case 200: kern = qmm_gemm_wr_kernel<XT, MODE, BITS, WD, 2>; nt = 256; break;
+          case 212: kern = qmm_gemm_wr_kernel<XT, MODE, BITS, WD, 2, 12>; nt = 256; break;
+        }
+      }
+      constexpr size_t lds = wr_lds_bytes<BITS>(WD);
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+      if (e != hipSuccess) return e;
+      hipLaunchKernelGGL(kern, grid, dim3(nt), lds, a.stream, a, ntm, ntn);
+    }
+  } else if (dma_ok && v8) {
+    auto kern = qmm_gemm_dma8_kernel<XT, MODE, BITS>;
+    constexpr size_t lds = dma_lds_bytes<BITS, MODE>();
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(kern, grid, dim3(512), lds, a.stream, a, ntm, ntn);
+  } else if (dma_ok) {
     auto kern = qmm_gemm_dma_kernel<XT, MODE, BITS>;
     constexpr size_t lds = dma_lds_bytes<BITS, MODE>();
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),

@@ -145,17 +145,6 @@ __device__ __forceinline__ f32x4_t mfma16x(const g_u32x4_t& a, const g_u32x4_t& 
                                                   __builtin_bit_cast(g_f16x8_t, b), c, 0, 0, 0);
 }
 
-// byte k of v as fp32 (v_cvt_f32_ubyte{k})
-template <int B>
-__device__ __forceinline__ float ubyte_f(uint32_t v) {
-  float r;
-  if constexpr (B == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(v));
-  else if constexpr (B == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(v));
-  else if constexpr (B == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(v));
-  else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(v));
-  return r;
-}
-
 // affine 4-bit chunk -> 16 packed pairs in natural order
 template <int XT>
 __device__ __forceinline__ void deq4_fast(const g_u32x4_t& wv, float s, float b, uint32_t (&o)[16]) {

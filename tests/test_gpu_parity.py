@@ -163,6 +163,21 @@ def test_qmm_fp_modes(ops, mode, M, xdt):
     assert rel_err(got, ref) <= TOL_FP[xdt]
 
 
+@pytest.mark.parametrize("xdt", ["bf16", "f16"])
+@pytest.mark.parametrize("M,N,K", [(100, 320, 1024), (300, 512, 256), (257, 96, 640), (520, 256, 1536)])
+@pytest.mark.parametrize("mode,bits,gs", [("affine", 4, 64), ("affine", 4, 32), ("affine", 4, 128),
+                                          ("affine", 8, 64), ("affine", 3, 64), ("mxfp4", 4, 32),
+                                          ("nvfp4", 4, 16), ("mxfp8", 8, 32)])
+def test_qmm_prefill_tiles(ops, mode, bits, gs, M, N, K, xdt):
+    # M > 64 takes the tiled GEMM; the K / group-count mix covers the
+    # chunked-load kernel (K % 128 == 0, 8 or 16 groups per scale chunk) and
+    # its fallbacks, ragged M and N edges, and K spans shorter than the ring
+    rng = np.random.default_rng(M + N + K + bits + gs)
+    got, ref = _qmm_case(ops, rng, M, N, K, xdt, mode=mode, bits=bits, gs=gs)
+    tol = TOL if mode == "affine" else TOL_FP
+    assert rel_err(got, ref) <= tol[xdt]
+
+
 @pytest.mark.parametrize("xdt", ["bf16", "f32"])
 @pytest.mark.parametrize("M", [1, 6, 100])
 @pytest.mark.parametrize("mode,bits,gs", [("affine", 4, 64), ("affine", 3, 32),
