@@ -4,28 +4,19 @@
 // x bf16 or fp16, fp32 accumulation.  Reference op: mlx/src/ops.rs:695-727
 // at prefill (x = [1, L, K], mlx/src/generate/mod.rs:76-80).
 //
-// Workgroup: 256 threads (4 waves, one per SIMD), output tile 256 x 256,
-// K step 64.  Each wave owns a 128 x 128 sub-tile as 4 x 4 blocks of
-// v_mfma_f32_32x32x16_{bf16,f16}; the 256 fp32 accumulators per lane live in
-// the unified VGPR/AGPR file (one wave per SIMD).
-//
-// Pipeline (one barrier per K step):
-//   - x tiles go global -> LDS directly (global_load_lds_dwordx4, no register
-//     staging) into a 3-stage ring, issued two steps ahead;
-//   - packed W tiles (8 KiB at 4 bits + scales) are fetched into registers
-//     two steps ahead, dequantized one step ahead with the same arithmetic as
-//     `dequantize` (rn(s*q + b); s*q is exact for 16-bit scales) and written
-//     as x's 16-bit type into a 2-stage ring.
-//   3 x 32 KiB (x) + 2 x 32 KiB (W) = the 160 KiB of LDS per CU.  Tiles are
-//   stored unpadded with 16-byte granules XOR-swizzled by (row / 2) mod 8, so
-//   the 16-byte fragment reads of 32 consecutive rows hit distinct banks.
-//   The step ends with s_waitcnt vmcnt(8) (everything but the 8 x loads just
-//   issued) and a bare s_barrier, so prefetches stay in flight across it.
-//
-// Workgroups are mapped so that consecutive tiles of an XCD share a column
-// block of W (its L2 keeps the dequantization inputs hot) and m varies
-// fastest.
+// Three kernels, all with 256 x 256 output tiles and fp32 accumulation in
+// v_mfma_f32_32x32x16_{bf16,f16}:
+//   - register-B kernel (transpose, 4- and 8-bit codes, K % 128 == 0 and the
+//     group count a multiple of one scale chunk): the prefill path;
+//   - eight-wave DMA kernel (other transposed shapes): dequantized W shared
+//     through an LDS ring;
+//   - register-staged kernel (transpose = false).
+// Dequantization uses the arithmetic of `dequantize` (s * q + b, or the fp
+// element times its scale) rounded once to x's 16-bit type.
+
 #include <stdlib.h>
+
+#include <atomic>
 
 #include <type_traits>
 
@@ -202,18 +193,12 @@ __global__ __launch_bounds__(256, 1) void qmm_gemm_reg_kernel(QmmArgs a, int ntm
 }
 
 // ---------------------------------------------------------------------------
-// DMA-pipelined kernel (transpose=true).  Every global read -- the x tile, the
-// packed W tile, its scales and biases -- is an LDS DMA
-// (global_load_lds_dword[x4]) issued DEPTH-1 = 3 K steps ahead into 4-stage
-// rings; no global data passes through registers, so the only waits are the
-// explicit s_waitcnt before each step's barrier.  Each step one thread
-// dequantizes one W row's 32 codes from the packed ring into a 2-stage bf16 /
-// fp16 ring (rn(s*q + b), the `dequantize` arithmetic), while the waves run
-// the step's MFMAs.  BK = 32; x and dequantized-W rows are 64 bytes (4
-// granules), granules XOR-swizzled so the fragment reads of consecutive rows
-// hit distinct banks.  One barrier per step: step k's MFMAs run interleaved
-// (sched_group_barrier) with the dequantization of step k+1, whose packed W
-// was made resident by the wait ending step k-1.
+// Shared pieces of the DMA kernels.  Every global read of x, packed W, scales
+// and biases is an LDS DMA (global_load_lds_dword[x4]) issued several K steps
+// ahead into rings, so no global data passes through registers and the only
+// waits are explicit s_waitcnt vmcnt before each step's barrier.  K step
+// (BK) = 32; x rows are 64 bytes (4 granules of 16 B), XOR-swizzled so the
+// fragment reads of 32 consecutive rows hit distinct banks.
 constexpr int DBK = 32, DEPTH = 4;
 constexpr int DA_STAGE = GBM * DBK;  // elements (16 KiB)
 constexpr int DB_STAGE = GBN * DBK;  // elements (16 KiB)
@@ -240,208 +225,25 @@ __device__ __forceinline__ void dma_x1(const void* g, uint32_t lds) {
                :: "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory", "m0");
 }
 
-template <int BITS, int MODE>
-struct DmaCounts {
-  static constexpr int X = 4;                              // x: 16 KiB / 4 waves / 1 KiB
-  static constexpr int W = BITS == 4 ? 1 : BITS;           // packed W per wave
-  static constexpr int S = MODE == AFFINE ? 2 : 1;         // scales (+ biases)
-  static constexpr int PER_STEP = X + W + S;
-  static constexpr int WBYTES = GBN * 4 * BITS;            // packed bytes per step
-};
-
-template <int XT, int MODE, int BITS>
-__global__ __launch_bounds__(256, 1) void qmm_gemm_dma_kernel(QmmArgs a, int ntm, int ntn) {
-  using XS = uint16_t;
-  using DC = DmaCounts<BITS, MODE>;
-  constexpr bool AFF = MODE == AFFINE;
-  extern __shared__ __attribute__((aligned(16))) uint16_t glds[];
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6, wm = wave >> 1, wn = wave & 1;
-  const int M = a.M, N = a.N, K = a.K;
-  const int nblk = ntm * ntn;
-  int bid = blockIdx.x;
-  if ((nblk & 7) == 0) bid = (bid & 7) * (nblk >> 3) + (bid >> 3);
-  const int tm = bid % ntm, tn = bid / ntm;
-  const int m0 = tm * GBM, n0 = tn * GBN;
-  const int64_t bb = blockIdx.y;
-  XS* out = static_cast<XS*>(a.out) + bb * static_cast<int64_t>(M) * N;
-  int64_t xb = 0, wb = 0;
-  if (a.bm.ndim != 0 || a.bm.lhs != nullptr || a.bm.rhs != nullptr) {
-    if (!map_batch(a.bm, bb, xb, wb)) {
-      for (int i = t; i < GBM * GBN; i += 256) {
-        const int r = m0 + i / GBN, c = n0 + i % GBN;
-        if (r < M && c < N) out[static_cast<int64_t>(r) * N + c] = from_f<XT>(__builtin_nanf(""));
-      }
-      return;
-    }
-  }
-  const XS* x = static_cast<const XS*>(a.x) + xb * a.x_mat;
-  const uint32_t* w = a.w + wb * a.w_mat;
-  const int gs = AFF ? a.gs : ModeInfo<MODE>::GS;
-  const int G = K / gs;
-  const int64_t wpr = static_cast<int64_t>(K) * BITS / 32;
-  const char* sbase = static_cast<const char*>(a.s) + wb * a.s_mat * (AFF ? 2 : 1);
-  const char* bbase = AFF ? static_cast<const char*>(a.b) + wb * a.s_mat * 2 : nullptr;
-
-  // LDS map (bytes): x ring | W-packed ring | scale ring | bias ring | deq-W ring
-  char* lbase = reinterpret_cast<char*>(glds);
-  char* xr = lbase;
-  char* wr = xr + DEPTH * DA_STAGE * 2;
-  char* sr = wr + DEPTH * DC::WBYTES;
-  char* br = sr + DEPTH * GBN * 4;
-  uint16_t* dq = reinterpret_cast<uint16_t*>(br + DEPTH * GBN * 4);
-
-  // ---- issue all DMA of K step `ks` into ring slot ks % DEPTH
-  auto issue = [&](int ks) {
-    const int slot = ks % DEPTH, k0 = ks * DBK;
-    // x: 16 rows x 64 B per instruction; wave covers rows [64 wave, +64)
-#pragma unroll
-    for (int i = 0; i < DC::X; ++i) {
-      const int rbase = wave * 64 + i * 16;
-      const int row = rbase + (lane >> 2);
-      const int g = ((lane & 3) ^ dswzf(row)) & 3;
-      const int gm = min(m0 + row, M - 1);
-      dma_x4(x + static_cast<int64_t>(gm) * K + k0 + g * 8,
-             __builtin_amdgcn_readfirstlane(lds_addr(xr + (slot * DA_STAGE + rbase * DBK) * 2)));
-    }
-    // packed W: the step's 4*BITS bytes of each of 256 rows
-    if constexpr (BITS == 4) {
-      const int row = wave * 64 + lane;
-      const int gn = min(n0 + row, N - 1);
-      dma_x4(w + gn * wpr + (k0 >> 5) * 4,
-             __builtin_amdgcn_readfirstlane(lds_addr(wr + slot * DC::WBYTES + wave * 64 * 16)));
-    } else {
-#pragma unroll
-      for (int i = 0; i < BITS; ++i) {
-        const int idx = (wave * BITS + i) * 64 + lane;      // word index in the stage
-        const int row = idx / BITS, word = idx - row * BITS;
-        const int gn = min(n0 + row, N - 1);
-        dma_x1(w + gn * wpr + (k0 >> 5) * BITS + word,
-               __builtin_amdgcn_readfirstlane(lds_addr(wr + slot * DC::WBYTES + (wave * BITS + i) * 256)));
-      }
-    }
-    // scales (and biases): the aligned dword holding this step's group
-    {
-      const int row = wave * 64 + lane;
-      const int gn = min(n0 + row, N - 1);
-      const int g = k0 / gs;
-      if constexpr (AFF) {
-        const int64_t e = static_cast<int64_t>(gn) * G + (g & ~1);
-        dma_x1(sbase + e * 2, __builtin_amdgcn_readfirstlane(lds_addr(sr + slot * GBN * 4 + wave * 256)));
-        dma_x1(bbase + e * 2, __builtin_amdgcn_readfirstlane(lds_addr(br + slot * GBN * 4 + wave * 256)));
-      } else {
-        const int64_t e = static_cast<int64_t>(gn) * G + (g & ~3);
-        dma_x1(sbase + e, __builtin_amdgcn_readfirstlane(lds_addr(sr + slot * GBN * 4 + wave * 256)));
-      }
-    }
-  };
-
-  // ---- dequantize step ks (ring slot ks % DEPTH) into deq slot ks & 1; thread = W row
-  auto dequant = [&](int ks) {
-    const int slot = ks % DEPTH, k0 = ks * DBK;
-    const int n = t;
-    uint32_t wd[BITS];
-    const uint32_t* wp = reinterpret_cast<const uint32_t*>(wr + slot * DC::WBYTES) + n * BITS;
-    if constexpr (BITS == 4) {
-      const g_u32x4_t v = *reinterpret_cast<const g_u32x4_t*>(wp);
-      wd[0] = v.x; wd[1] = v.y; wd[2] = v.z; wd[3] = v.w;
-    } else {
-#pragma unroll
-      for (int i = 0; i < BITS; ++i) wd[i] = wp[i];
-    }
-    const int g = k0 / gs;
-    const uint32_t sw = reinterpret_cast<const uint32_t*>(sr + slot * GBN * 4)[n];
-    float s, b = 0.f, s2;
-    if constexpr (AFF) {
-      const uint16_t sh = static_cast<uint16_t>((g & 1) ? (sw >> 16) : (sw & 0xffffu));
-      const uint32_t bw = reinterpret_cast<const uint32_t*>(br + slot * GBN * 4)[n];
-      const uint16_t bh = static_cast<uint16_t>((g & 1) ? (bw >> 16) : (bw & 0xffffu));
-      s = to_f<XT>(sh);
-      b = to_f<XT>(bh);
-      s2 = s;
-    } else {
-      s = fp_scale<MODE>((sw >> (8 * (g & 3))) & 0xffu);
-      s2 = MODE == NVFP4 ? fp_scale<MODE>((sw >> (8 * ((g + 1) & 3))) & 0xffu) : s;
-    }
-    uint32_t o[16];
-    dequant32<XT, MODE, BITS>(wd, s, b, s2, o);
-    uint16_t* B = dq + (ks & 1) * DB_STAGE;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      *reinterpret_cast<g_u32x4_t*>(&B[dswz(n, 8 * i)]) =
-          g_u32x4_t{o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]};
-  };
-
-  f32x16_t acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
-
-  const int nk = K / DBK;
-  // prologue: steps 0 .. DEPTH-2 in flight; step 0 dequantized; step 1 resident
-  for (int ks = 0; ks < DEPTH - 1 && ks < nk; ++ks) issue(ks);
-  asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-  dequant(0);
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-
-  for (int ks = 0; ks < nk; ++ks) {
-    if (ks + DEPTH - 1 < nk) issue(ks + DEPTH - 1);
-    const uint16_t* Ast = reinterpret_cast<const uint16_t*>(xr) + (ks % DEPTH) * DA_STAGE;
-    const uint16_t* Bst = dq + (ks & 1) * DB_STAGE;
-#pragma unroll
-    for (int kk = 0; kk < DBK / 16; ++kk) {
-      const int kq = kk * 16 + 8 * (lane >> 5);
-      g_u32x4_t af[4], bf[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        af[i] = *reinterpret_cast<const g_u32x4_t*>(&Ast[dswz(wm * 128 + i * 32 + (lane & 31), kq)]);
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        bf[j] = *reinterpret_cast<const g_u32x4_t*>(&Bst[dswz(wn * 128 + j * 32 + (lane & 31), kq)]);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = mfma32<XT>(af[i], bf[j], acc[i][j]);
-    }
-    if (ks + 1 < nk) dequant(ks + 1);
-    // interleave: fragment reads first, then MFMA / VALU / LDS groups
-    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);   // 8 DS reads (kk = 0 fragments)
-#pragma unroll
-    for (int g = 0; g < 32; ++g) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // 1 MFMA
-      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // 4 VALU
-      if (g % 4 == 3) __builtin_amdgcn_sched_group_barrier(0x300, 2, 0);  // DS read/write
-    }
-    // end of step: everything but the last issued step's DMA is resident
-    if (ks + 2 < nk) {
-      if (ks + DEPTH - 1 < nk) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" :: "n"(DC::PER_STEP) : "memory");
-      else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    } else {
-      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    }
-  }
-
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int col = n0 + wn * 128 + j * 32 + (lane & 31);
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int row = m0 + wm * 128 + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-        if (row < M && col < N) out[static_cast<int64_t>(row) * N + col] = from_f<XT>(acc[i][j][v]);
-      }
-    }
+// DMA with a wave-uniform 64-bit base (SGPRs) and a 32-bit per-lane offset
+__device__ __forceinline__ void dma_x4s(uint32_t voff, const void* sbase, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :: "v"(voff), "s"(sbase), "s"(lds) : "memory", "m0");
 }
 
+template <int BITS, int MODE>
+struct DmaCounts {
+  static constexpr int WBYTES = GBN * 4 * BITS;            // packed W bytes per step
+};
+
 // ---------------------------------------------------------------------------
-// Eight-wave DMA kernel: the same pipeline with 512 threads, two waves per
-// SIMD, each wave owning a 64 x 128 sub-tile (2 x 4 blocks of 32 x 32), so one
-// wave's MFMAs overlap the other's dequantization, LDS waits and barrier.
-// DMA instructions are spread round-robin over the waves; each wave waits on
-// its own issue count (wait_vm).
+// Eight-wave DMA kernel: 512 threads, two waves per SIMD, each wave owning a
+// 64 x 128 sub-tile (2 x 4 blocks of 32 x 32).  Per step one thread
+// dequantizes 16 codes of one W row from the packed ring into a 2-stage bf16 /
+// fp16 ring that all waves read; step k's MFMAs run interleaved
+// (sched_group_barrier) with the dequantization of step k+1, whose packed W
+// was made resident by the wait ending step k-1.  DMA instructions are spread
+// round-robin over the waves; each wave waits on its own issue count.
 __device__ __forceinline__ void wait_vm(int n) {
   switch (n) {
     case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
@@ -754,14 +556,32 @@ struct WrCfg {
   static constexpr int WSL = BITS == 4 ? 2 : 3;
 };
 
-template <int XT, int MODE, int BITS, int WD, int NCB, int ABL = 0>
-__global__ __launch_bounds__(512 / NCB, 1) void qmm_gemm_wr_kernel(QmmArgs a, int ntm, int ntn) {
+// Tile order: workgroup ids are first made contiguous per XCD (the hardware
+// deals consecutive ids round-robin over the 8 XCDs), then walked in groups of
+// GM row tiles, m fastest, so each XCD's L2 holds a GM-tile strip of x and the
+// W column tiles in flight.
+template <int GM>
+__device__ __forceinline__ void tile_of(int bid, int ntm, int ntn, int& tm, int& tn) {
+  const int nblk = ntm * ntn;
+  if ((nblk & 7) == 0) bid = (bid & 7) * (nblk >> 3) + (bid >> 3);
+  const int per = GM * ntn;
+  const int grp = bid / per, first = grp * GM;
+  const int gsz = min(ntm - first, GM);
+  const int r = bid - grp * per;
+  tm = first + r % gsz;
+  tn = r / gsz;
+}
+
+template <int XT, int MODE, int BITS, int WD, int NCB, int RB>
+__global__ __launch_bounds__(64 * (8 / RB) * (8 / NCB), 1) void qmm_gemm_wr_kernel(QmmArgs a, int ntm, int ntn) {
   static_assert(BITS == 4 || BITS == 8, "register-B kernel takes 4- and 8-bit codes");
-  static_assert(WD % 2 == 0 && WD >= 6, "B double buffer alternates with the x slot");
+  static_assert(WD % 2 == 0 && WD >= 4, "B double buffer alternates with the x slot");
   using XS = uint16_t;
   using CF = WrCfg<BITS>;
   constexpr bool AFF = MODE == AFFINE;
-  constexpr int NW = 8 / NCB;          // waves; wave w owns columns [32 NCB w, 32 NCB (w + 1))
+  // waves: NWN across N (32 NCB columns each) x 8 / RB across M (32 RB rows each)
+  constexpr int NWN = 8 / NCB;
+  constexpr int NW = NWN * (8 / RB);
   constexpr int NT = 64 * NW;
   constexpr int XI = 16 / NW;           // x / W-chunk DMA instructions per wave
   constexpr int SI = AFF ? 8 / NW : (NW >= 4 ? 1 : 4 / NW);  // scale-chunk instructions (waves < SW)
@@ -770,11 +590,10 @@ __global__ __launch_bounds__(512 / NCB, 1) void qmm_gemm_wr_kernel(QmmArgs a, in
   extern __shared__ __attribute__((aligned(16))) uint16_t glds[];
   const int t = threadIdx.x, lane = t & 63, h = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);  // uniform: keeps DMA counts scalar
+  const int wn = wave % NWN, wm = wave / NWN;
   const int M = a.M, N = a.N, K = a.K;
-  const int nblk = ntm * ntn;
-  int bid = blockIdx.x;
-  if ((nblk & 7) == 0) bid = (bid & 7) * (nblk >> 3) + (bid >> 3);
-  const int tm = bid % ntm, tn = bid / ntm;
+  int tm, tn;
+  tile_of<4>(blockIdx.x, ntm, ntn, tm, tn);
   const int m0 = tm * GBM, n0 = tn * GBN;
   const int64_t bb = blockIdx.y;
   XS* out = static_cast<XS*>(a.out) + bb * static_cast<int64_t>(M) * N;
@@ -806,39 +625,41 @@ __global__ __launch_bounds__(512 / NCB, 1) void qmm_gemm_wr_kernel(QmmArgs a, in
   char* lb = reinterpret_cast<char*>(glds);
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(lb));
 
-  // ---- DMA sources at k = 0 and wave-uniform destinations
-  const XS* xsrc[XI];
-  uint32_t xdst_s[XI];
+  // ---- DMA: wave-uniform bases (SGPRs, advanced per step) + per-lane 32-bit
+  // offsets within the tile, and wave-uniform LDS destinations
+  const char* xtile = reinterpret_cast<const char*>(x + static_cast<int64_t>(m0) * K);
+  uint32_t xoff[XI], xdst_s[XI];
 #pragma unroll
   for (int i = 0; i < XI; ++i) {
     const int rbase = (wave + NW * i) * 16;
     const int row = rbase + (lane >> 2);
     const int g = ((lane & 3) ^ dswzf(row)) & 3;
-    xsrc[i] = x + static_cast<int64_t>(min(m0 + row, M - 1)) * K + g * 8;
+    xoff[i] = static_cast<uint32_t>((min(m0 + row, M - 1) - m0) * K * 2 + g * 16);
     xdst_s[i] = __builtin_amdgcn_readfirstlane(lds0 + XR + rbase * DBK * 2);
   }
   // W chunk: 256 rows x 4 granules = 16 instructions; stored granule p of
   // row r holds logical granule p ^ f(r)
-  const char* wsrc[XI];
-  uint32_t wdst_s[XI];
+  const char* wtile = w + static_cast<int64_t>(n0) * wrow;
+  uint32_t woff[XI], wdst_s[XI];
 #pragma unroll
   for (int i = 0; i < XI; ++i) {
     const int j = wave + NW * i;
     const int row = j * 16 + (lane >> 2);
     const int g = ((lane & 3) ^ dswzf(row)) & 3;
-    wsrc[i] = w + static_cast<int64_t>(min(n0 + row, N - 1)) * wrow + g * 16;
+    woff[i] = static_cast<uint32_t>((min(n0 + row, N - 1) - n0) * wrow + g * 16);
     wdst_s[i] = __builtin_amdgcn_readfirstlane(lds0 + WR + j * 1024);
   }
   // scale chunk: 64 rows x 16 B per instruction; 4 instructions of scales
   // (+ 4 of biases), instruction q = wave + NW i on waves < SW
   const int my_s = wave < SW ? SI : 0;
-  const char* ssrc[SI];
-  uint32_t sdst_s[SI];
+  const char* stile[SI];
+  uint32_t soff[SI], sdst_s[SI];
 #pragma unroll
   for (int i = 0; i < SI; ++i) {
     const int q = min(wave + NW * i, AFF ? 7 : 3);
     const int srow = min(n0 + (q & 3) * 64 + lane, N - 1);
-    ssrc[i] = ((AFF && q >= 4) ? bbase : sbase) + static_cast<int64_t>(srow) * G * ssz;
+    stile[i] = ((AFF && q >= 4) ? bbase : sbase) + static_cast<int64_t>(n0) * G * ssz;
+    soff[i] = static_cast<uint32_t>((srow - n0) * G * ssz);
     sdst_s[i] = __builtin_amdgcn_readfirstlane(lds0 + (AFF && q >= 4 ? BR : SR) + (q & 3) * 1024);
   }
   const int gshift = __builtin_ctz(gs);
@@ -851,25 +672,26 @@ __global__ __launch_bounds__(512 / NCB, 1) void qmm_gemm_wr_kernel(QmmArgs a, in
   auto issue = [&](int j, auto slot_c, auto wchunk_c) {
     constexpr int SL = decltype(slot_c)::value;
     constexpr bool WCH = decltype(wchunk_c)::value;
-    const int k0 = (ABL & 2) ? 0 : j * DBK;
-    if (ABL & 8) return;
+    const int k0 = j * DBK;
+    const char* xk = xtile + k0 * 2;
 #pragma unroll
-    for (int i = 0; i < XI; ++i) dma_x4(xsrc[i] + k0, xdst_s[i] + SL * DA_STAGE * 2);
+    for (int i = 0; i < XI; ++i) dma_x4s(xoff[i], xk, xdst_s[i] + SL * DA_STAGE * 2);
     if constexpr (WCH) {
       const uint32_t wsl = ((j >> WCS) % CF::WSL) * CF::WSLOT;
+      const char* wk = wtile + (k0 >> 5) * CF::STEP_B;
 #pragma unroll
-      for (int i = 0; i < XI; ++i) dma_x4(wsrc[i] + (k0 >> 5) * CF::STEP_B, wdst_s[i] + wsl);
+      for (int i = 0; i < XI; ++i) dma_x4s(woff[i], wk, wdst_s[i] + wsl);
     }
     if ((j & ((1 << pshift) - 1)) == 0 && my_s) {
       const int g0 = k0 >> gshift;
 #pragma unroll
-      for (int i = 0; i < SI; ++i) dma_x4(ssrc[i] + g0 * ssz, sdst_s[i] + ((j >> pshift) & 1) * SSLOT);
+      for (int i = 0; i < SI; ++i) dma_x4s(soff[i], stile[i] + g0 * ssz, sdst_s[i] + ((j >> pshift) & 1) * SSLOT);
     }
   };
 
   // ---- B fragments of step ks for column cn of the tile
   auto deq_b = [&](int ks, int cb, g_u32x4_t (&bo)[2]) {
-    const int cn = 32 * (NCB * wave + cb) + (lane & 31);
+    const int cn = 32 * (NCB * wn + cb) + (lane & 31);
     const int wsw = dswzf(cn);
     const int g = (ks * DBK) >> gshift;
     const char* ch = lb + WR + ((ks >> WCS) % CF::WSL) * CF::WSLOT;
@@ -932,11 +754,11 @@ __global__ __launch_bounds__(512 / NCB, 1) void qmm_gemm_wr_kernel(QmmArgs a, in
   // swizzle depends on row % 32 only, so block i is +i * 32 rows.
   int offA[2];
 #pragma unroll
-  for (int kk = 0; kk < 2; ++kk) offA[kk] = dswz(lane & 31, 16 * h + 8 * kk) * 2;
+  for (int kk = 0; kk < 2; ++kk) offA[kk] = dswz(lane & 31, 16 * h + 8 * kk) * 2 + wm * RB * 32 * DBK * 2;
 
-  f32x16_t acc[8][NCB];
+  f32x16_t acc[RB][NCB];
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < RB; ++i)
 #pragma unroll
     for (int c = 0; c < NCB; ++c)
 #pragma unroll
@@ -945,13 +767,13 @@ __global__ __launch_bounds__(512 / NCB, 1) void qmm_gemm_wr_kernel(QmmArgs a, in
   // MFMAs of one step; each A fragment register is refilled with the next
   // step's fragment (slot sn, resident since the previous barrier) right after
   // its last use, so the next step starts with its operands in flight.
-  auto mfma_step = [&](const g_u32x4_t (&bf)[NCB][2], g_u32x4_t (&af)[2][8], auto sn_c) {
+  auto mfma_step = [&](const g_u32x4_t (&bf)[NCB][2], g_u32x4_t (&af)[2][RB], auto sn_c) {
     constexpr int SN = decltype(sn_c)::value;
     const char* An = lb + XR + SN * DA_STAGE * 2;
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < RB; ++i) {
 #pragma unroll
         for (int c = 0; c < NCB; ++c) acc[i][c] = mfma32<XT>(af[kk][i], bf[c][kk], acc[i][c]);
         af[kk][i] = *reinterpret_cast<const g_u32x4_t*>(An + offA[kk] + i * 32 * DBK * 2);
@@ -965,13 +787,13 @@ __global__ __launch_bounds__(512 / NCB, 1) void qmm_gemm_wr_kernel(QmmArgs a, in
   // slots are refilled only after every reader of their previous chunk has
   // passed a barrier ((WSL - 1) WC > WD - 3 and P > WD - 3 steps).
   const int nk = K / DBK;
-  g_u32x4_t bq[2][NCB][2], af[2][8];
+  g_u32x4_t bq[2][NCB][2], af[2][RB];
   static_for<0, WD - 1>([&](auto s_c) {
     constexpr int J = decltype(s_c)::value;
     if (J < nk) issue(J, s_c, std::integral_constant<bool, J % CF::WC == 0>{});
   });
   // steps 0 and 1 resident: DMAs of steps 2 .. WD-2 may stay in flight
-  if (!(ABL & 8)) {
+  {
     if (nk >= WD - 1) {
       constexpr int nx = [] {
         int n = 0;
@@ -991,7 +813,7 @@ __global__ __launch_bounds__(512 / NCB, 1) void qmm_gemm_wr_kernel(QmmArgs a, in
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
+      for (int i = 0; i < RB; ++i)
         af[kk][i] = *reinterpret_cast<const g_u32x4_t*>(Ast + offA[kk] + i * 32 * DBK * 2);
   }
 
@@ -1009,12 +831,10 @@ __global__ __launch_bounds__(512 / NCB, 1) void qmm_gemm_wr_kernel(QmmArgs a, in
         if (steady)
           issue(ks + WD - 1, std::integral_constant<int, (S + WD - 1) % WD>{},
                 std::integral_constant<bool, (S + WD - 1) % CF::WC == 0>{});
-        if (!(ABL & 4)) {
 #pragma unroll
-          for (int c = 0; c < NCB; ++c) deq_b(ks + 1, c, bq[(S + 1) & 1][c]);
-        }
-        if (!(ABL & 1)) mfma_step(bq[S & 1], af, std::integral_constant<int, (S + 1) % WD>{});
-        if (!(ABL & 8)) {
+        for (int c = 0; c < NCB; ++c) deq_b(ks + 1, c, bq[(S + 1) & 1][c]);
+        mfma_step(bq[S & 1], af, std::integral_constant<int, (S + 1) % WD>{});
+        {
           if (steady) {
             // DMAs of steps ks+3 .. ks+WD-1 may stay in flight
             constexpr int nx = [] {
@@ -1035,15 +855,34 @@ __global__ __launch_bounds__(512 / NCB, 1) void qmm_gemm_wr_kernel(QmmArgs a, in
     });
   }
 
+  if (m0 + 32 * RB * (wm + 1) <= M) {
+    // full row tile: wave-uniform row bases (SGPRs) + one 32-bit lane offset
+#pragma unroll
+    for (int c = 0; c < NCB; ++c) {
+      const int col = n0 + 32 * (NCB * wn + c) + (lane & 31);
+      const uint32_t voff = static_cast<uint32_t>((4 * h * N + col) * 2);
+      if (col < N) {
+#pragma unroll
+        for (int i = 0; i < RB; ++i)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const XS* ub = out + static_cast<int64_t>(m0 + (RB * wm + i) * 32 + 8 * (v >> 2) + (v & 3)) * N;
+            const uint32_t d = from_f<XT>(acc[i][c][v]);
+            asm volatile("global_store_short %0, %1, %2" ::"v"(voff), "v"(d), "s"(ub) : "memory");
+          }
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int c = 0; c < NCB; ++c) {
-    const int col = n0 + 32 * (NCB * wave + c) + (lane & 31);
+    const int col = n0 + 32 * (NCB * wn + c) + (lane & 31);
     if (col < N) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
+      for (int i = 0; i < RB; ++i)
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-          const int row = m0 + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+          const int row = m0 + (RB * wm + i) * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
           if (row < M) out[static_cast<int64_t>(row) * N + col] = from_f<XT>(acc[i][c][v]);
         }
     }
@@ -1066,6 +905,21 @@ bool qmm_gemm_supported(const QmmArgs& a) {
 }
 
 namespace {
+// Raise a kernel's dynamic-LDS limit once per device; the attribute persists,
+// and setting it on every launch costs host time on the launch path.
+template <auto KERN>
+hipError_t set_lds_once(size_t bytes) {
+  static std::atomic<uint64_t> done{0};  // one bit per device id < 64
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 64;
+  const uint64_t bit = dev < 64 ? (1ull << dev) : 0;
+  if (bit && (done.load(std::memory_order_acquire) & bit)) return hipSuccess;
+  const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(KERN),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e == hipSuccess && bit) done.fetch_or(bit, std::memory_order_release);
+  return e;
+}
+
 template <int XT, int MODE, int BITS>
 hipError_t gemm_launch_t(const QmmArgs& a) {
   const int ntm = (a.M + GBM - 1) / GBM, ntn = (a.N + GBN - 1) / GBN;
@@ -1075,55 +929,32 @@ hipError_t gemm_launch_t(const QmmArgs& a) {
   const dim3 grid(static_cast<unsigned>(nblk), static_cast<unsigned>(a.nbatch));
   const int G = a.K / (MODE == AFFINE ? a.gs : ModeInfo<MODE>::GS);
   const bool dma_ok = a.transpose && a.K % DBK == 0 && (MODE == AFFINE ? G % 2 == 0 : G % 4 == 0);
-  static const int v8 = [] { const char* e = getenv("IQMM_TUNE_GEMM8"); return e ? atoi(e) : 2; }();
-  static const int abl = [] { const char* e = getenv("IQMM_ABL"); return e ? atoi(e) : 0; }();
   constexpr int WD = 6;
   constexpr int GPC = MODE == AFFINE ? 8 : 16;
   const bool wr_ok = dma_ok && (BITS == 4 || BITS == 8) && a.K % (32 * (BITS == 4 ? 4 : 2)) == 0 &&
                      G % GPC == 0;
-  if (wr_ok && v8 == 2) {
+  if (wr_ok) {
     if constexpr (BITS == 4 || BITS == 8) {
-      auto kern = qmm_gemm_wr_kernel<XT, MODE, BITS, WD, 1>;
-      int nt = 512;
-      if constexpr (XT == BF16 && MODE == AFFINE && BITS == 4) {
-        switch (abl) {
-          case 1: kern = qmm_gemm_wr_kernel<XT, MODE, BITS, WD, 1, 1>; break;
-          case 8: kern = qmm_gemm_wr_kernel<XT, MODE, BITS, WD, 1, 8>; break;
-          case 12: kern = qmm_gemm_wr_kernel<XT, MODE, BITS, WD, 1, 12>; break;
-          case 200: kern = qmm_gemm_wr_kernel<XT, MODE, BITS, WD, 2>; nt = 256; break;
-          case 212: kern = qmm_gemm_wr_kernel<XT, MODE, BITS, WD, 2, 12>; nt = 256; break;
-        }
-      }
+      constexpr auto kern = qmm_gemm_wr_kernel<XT, MODE, BITS, WD, 1, 8>;
       constexpr size_t lds = wr_lds_bytes<BITS>(WD);
-      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+      hipError_t e = set_lds_once<kern>(lds);
       if (e != hipSuccess) return e;
-      hipLaunchKernelGGL(kern, grid, dim3(nt), lds, a.stream, a, ntm, ntn);
+      hipLaunchKernelGGL(kern, grid, dim3(512), lds, a.stream, a, ntm, ntn);
     }
-  } else if (dma_ok && v8) {
-    auto kern = qmm_gemm_dma8_kernel<XT, MODE, BITS>;
+  } else if (dma_ok) {
+    constexpr auto kern = qmm_gemm_dma8_kernel<XT, MODE, BITS>;
     constexpr size_t lds = dma_lds_bytes<BITS, MODE>();
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    hipError_t e = set_lds_once<kern>(lds);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(kern, grid, dim3(512), lds, a.stream, a, ntm, ntn);
-  } else if (dma_ok) {
-    auto kern = qmm_gemm_dma_kernel<XT, MODE, BITS>;
-    constexpr size_t lds = dma_lds_bytes<BITS, MODE>();
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(kern, grid, dim3(256), lds, a.stream, a, ntm, ntn);
   } else if (a.transpose) {
-    auto kern = qmm_gemm_reg_kernel<XT, MODE, BITS, true>;
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, REG_LDS_BYTES);
+    constexpr auto kern = qmm_gemm_reg_kernel<XT, MODE, BITS, true>;
+    hipError_t e = set_lds_once<kern>(REG_LDS_BYTES);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(kern, grid, dim3(256), REG_LDS_BYTES, a.stream, a, ntm, ntn);
   } else {
-    auto kern = qmm_gemm_reg_kernel<XT, MODE, BITS, false>;
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, REG_LDS_BYTES);
+    constexpr auto kern = qmm_gemm_reg_kernel<XT, MODE, BITS, false>;
+    hipError_t e = set_lds_once<kern>(REG_LDS_BYTES);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(kern, grid, dim3(256), REG_LDS_BYTES, a.stream, a, ntm, ntn);
   }
