@@ -1,6 +1,6 @@
-// qmv_q4.hip — the decode GEMV fast path: affine 4-bit, transpose=true, M=1,
-// bf16 or fp16 activations (the shape every ironmlx decode step runs,
-// mlx/src/nn/linear.rs:51-63 with x = [1, 1, K]).
+// qmv_q4.hip — the decode GEMV fast path: affine 4-bit, transpose=true,
+// M = 1..3 rows of bf16 or fp16 activations (the shape every ironmlx decode
+// step runs, mlx/src/nn/linear.rs:51-63 with x = [1, 1, K]).
 //
 // One wave per workgroup owns RB (1, 2 or 4) consecutive weight rows.  Lane
 // l owns the 32-code chunks c = l, l+64, ... (CPL of them) of every row: a
@@ -96,118 +96,217 @@ __device__ __forceinline__ float chunk_dot(const u32x4_t& wv, const uint32_t (&P
   return d;
 }
 
+// The W half of chunk_dot: the 16 (C + n) pairs of one chunk, reused for
+// every x row of a multi-row GEMV.
+template <int XT>
+__device__ __forceinline__ void chunk_pairs(const u32x4_t& wv, uint32_t (&W)[16]) {
+  const uint32_t E = Magic<XT>::ebytes;
+  const uint32_t wd[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const uint32_t lo = wd[q] & 0x0F0F0F0Fu;
+    const uint32_t hi = (wd[q] >> 4) & 0x0F0F0F0Fu;
+    W[4 * q + 0] = __builtin_amdgcn_perm(E, lo, SEL_B0B2);
+    W[4 * q + 1] = __builtin_amdgcn_perm(E, lo, SEL_B1B3);
+    W[4 * q + 2] = __builtin_amdgcn_perm(E, hi, SEL_B0B2);
+    W[4 * q + 3] = __builtin_amdgcn_perm(E, hi, SEL_B1B3);
+  }
+}
+
 // ---------------------------------------------------------------------------
-// Ordered single-pass kernel (the default).  One wave per workgroup owns RB
-// rows; lane l owns chunks l, l+64, ... (CPL per row).  Loads are issued in
-// the order they are consumed -- x first (cache-resident), then for each row
-// its weight chunks followed by its scales and biases -- so that, with
-// in-order vmcnt accounting, row r's arithmetic and DPP reduction run while
-// the loads of rows r+1.. are still in flight.
-template <int XT, int RB, int CPL>
-__global__ __launch_bounds__(64) void qmv_q4_ord_kernel(QmmArgs a, int64_t batch0) {
+// Single-pass kernel.  One wave per workgroup owns RB rows; lane l owns
+// chunks l, l+64, ... (CPL per row).  Every load is issued before any
+// arithmetic -- x first (cache-resident), then for each row its weight chunks
+// followed by its scales and biases -- and a scheduling barrier keeps the
+// compiler from sinking loads behind the first wait, so with in-order vmcnt
+// accounting row r's arithmetic and DPP reduction run while the loads of rows
+// r+1.. are still in flight.  The arguments are a compact block (one scalar
+// load); the general batch map is read only by the MAPPED instantiation.
+struct Q4Args {
+  const char* x;
+  const char* w;
+  const char* s;
+  const char* b;
+  char* out;
+  int N, K, gshift, pad;
+  int64_t x_mat, w_mat, s_mat;  // byte strides between batch elements
+};
+
+template <int XT, int RB, int CPL, bool MAPPED, int MR>
+__global__ __launch_bounds__(64) void qmv_q4_kernel(Q4Args p, BatchMap bm, int64_t batch0) {
   using XS = uint16_t;
   const int lane = threadIdx.x;
   const int64_t bb = batch0 + blockIdx.y;
-  const int N = a.N, K = a.K, C = K >> 5;
-  XS* out = static_cast<XS*>(a.out) + bb * static_cast<int64_t>(N);
+  const int N = p.N, K = p.K, C = K >> 5;
+  XS* out = reinterpret_cast<XS*>(p.out) + bb * static_cast<int64_t>(N) * MR;
   const int row0 = blockIdx.x * RB;
 
-  int64_t xb = 0, wb = 0;
-  if (a.bm.ndim != 0 || a.bm.lhs != nullptr || a.bm.rhs != nullptr) {
-    if (!map_batch(a.bm, bb, xb, wb)) {
-      if (lane < RB && row0 + lane < N) out[row0 + lane] = from_f<XT>(__builtin_nanf(""));
+  int64_t xi = bb, wi = bb;
+  if constexpr (MAPPED) {
+    if (!map_batch(bm, bb, xi, wi)) {
+      if (lane < RB * MR && row0 + lane % RB < N)
+        out[static_cast<int64_t>(lane / RB) * N + row0 + lane % RB] = from_f<XT>(__builtin_nanf(""));
       return;
     }
   }
-  const char* xbase = reinterpret_cast<const char*>(static_cast<const XS*>(a.x) + xb * a.x_mat);
-  const uint32_t* w = a.w + wb * a.w_mat;
-  const XS* sp = static_cast<const XS*>(a.s) + wb * a.s_mat;
-  const XS* bp = static_cast<const XS*>(a.b) + wb * a.s_mat;
-  const int wpr = K >> 3, G = K / a.gs, gshift = __builtin_ctz(a.gs);
+  const char* xbase = p.x + xi * p.x_mat;
+  const char* w = p.w + wi * p.w_mat;
+  const char* sp = p.s + wi * p.s_mat;
+  const char* bp = p.b + wi * p.s_mat;
+  // bytes per row; one matrix's packed codes and scales stay below 4 GiB
+  // (checked by the launcher), so row offsets are 32-bit scalar products
+  const uint32_t wrow = static_cast<uint32_t>(K) >> 1, srow = (static_cast<uint32_t>(K) >> p.gshift) * 2;
+  const uint32_t xrow = static_cast<uint32_t>(K) * 2;
 
-  // chunk index per slot (clamped; out-of-range slots are masked at the end)
-  int cidx[CPL];
+  // per-lane byte offsets (32-bit) of each slot's chunk, x chunk and group
+  uint32_t cw[CPL], cx[CPL], cg[CPL];
 #pragma unroll
-  for (int j = 0; j < CPL; ++j) cidx[j] = min(lane + 64 * j, C - 1);
+  for (int j = 0; j < CPL; ++j) {
+    const uint32_t cidx = static_cast<uint32_t>(min(lane + 64 * j, C - 1));
+    cw[j] = cidx << 4;
+    cx[j] = cidx << 6;
+    cg[j] = ((cidx << 5) >> p.gshift) * 2;
+  }
 
   // 1. x chunks (cache-resident) first
-  uint32_t X[CPL][16];
+  u32x4_t xv[MR][CPL][4];
 #pragma unroll
-  for (int j = 0; j < CPL; ++j)
+  for (int m = 0; m < MR; ++m)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(xbase + (cidx[j] << 6) + 16 * i);
-      X[j][4 * i] = v.x; X[j][4 * i + 1] = v.y; X[j][4 * i + 2] = v.z; X[j][4 * i + 3] = v.w;
-    }
-  // 2. per row: weight chunks, then that row's scales / biases
+    for (int j = 0; j < CPL; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        xv[m][j][i] = *reinterpret_cast<const u32x4_t*>(xbase + m * xrow + cx[j] + 16 * i);
+  // 2. per row: weight chunks, then that row's scales / biases (row bases are
+  //    wave-uniform, so every load is scalar base + 32-bit lane offset)
   u32x4_t wv[RB][CPL];
   XS sr[RB][CPL], br[RB][CPL];
 #pragma unroll
   for (int r = 0; r < RB; ++r) {
-    const int row = min(row0 + r, N - 1);
-    const char* wr = reinterpret_cast<const char*>(w + static_cast<int64_t>(row) * wpr);
-    const XS* srow = sp + static_cast<int64_t>(row) * G;
-    const XS* brow = bp + static_cast<int64_t>(row) * G;
+    const uint32_t row = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(min(row0 + r, N - 1)));
+    const char* wr = w + row * wrow;
+    const char* sr_ = sp + row * srow;
+    const char* br_ = bp + row * srow;
 #pragma unroll
     for (int j = 0; j < CPL; ++j)
-      wv[r][j] = __builtin_nontemporal_load(
-          reinterpret_cast<const u32x4_t*>(wr + (static_cast<uint32_t>(cidx[j]) << 4)));
+      wv[r][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(wr + cw[j]));
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-      const int g = (cidx[j] << 5) >> gshift;
-      sr[r][j] = srow[g];
-      br[r][j] = brow[g];
+      sr[r][j] = *reinterpret_cast<const XS*>(sr_ + cg[j]);
+      br[r][j] = *reinterpret_cast<const XS*>(br_ + cg[j]);
     }
   }
+  __builtin_amdgcn_sched_barrier(0);
   // 3. x pairs and chunk sums (overlaps the weight loads)
-  uint32_t P[CPL][16];
-  float xs[CPL];
+  uint32_t P[MR][CPL][16];
+  float xs[MR][CPL];
 #pragma unroll
-  for (int j = 0; j < CPL; ++j) {
-    make_pairs<XT>(X[j], P[j], xs[j]);
-    if (lane + 64 * j >= C) xs[j] = 0.f;  // masked slot contributes nothing
-  }
+  for (int m = 0; m < MR; ++m)
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      uint32_t X[16];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        X[4 * i] = xv[m][j][i].x; X[4 * i + 1] = xv[m][j][i].y;
+        X[4 * i + 2] = xv[m][j][i].z; X[4 * i + 3] = xv[m][j][i].w;
+      }
+      make_pairs<XT>(X, P[m][j], xs[m][j]);
+      if (lane + 64 * j >= C) xs[m][j] = 0.f;  // masked slot contributes nothing
+    }
   // 4. rows in load order
 #pragma unroll
   for (int r = 0; r < RB; ++r) {
-    float acc = 0.f;
+    float acc[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) acc[m] = 0.f;
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-      float d = chunk_dot<XT>(wv[r][j], P[j]);
-      if (lane + 64 * j >= C) d = 0.f;
+      const bool live = lane + 64 * j < C;
       const float s = to_f<XT>(sr[r][j]), b = to_f<XT>(br[r][j]);
-      acc = fmaf(s, fmaf(-Magic<XT>::c, xs[j], d), fmaf(b, xs[j], acc));
+      if constexpr (MR == 1) {
+        float d = chunk_dot<XT>(wv[r][j], P[0][j]);
+        if (!live) d = 0.f;
+        acc[0] = fmaf(s, fmaf(-Magic<XT>::c, xs[0][j], d), fmaf(b, xs[0][j], acc[0]));
+      } else {
+        uint32_t Wp[16];
+        chunk_pairs<XT>(wv[r][j], Wp);
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+          float d = 0.f;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) d = dot2<XT>(Wp[i], P[m][j][i], d);
+          if (!live) d = 0.f;
+          acc[m] = fmaf(s, fmaf(-Magic<XT>::c, xs[m][j], d), fmaf(b, xs[m][j], acc[m]));
+        }
+      }
     }
-    acc = dpp_sum_to_lane63(acc);
-    if (lane == 63 && row0 + r < N) out[row0 + r] = from_f<XT>(acc);
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      const float v = dpp_sum_to_lane63(acc[m]);
+      if (lane == 63 && row0 + r < N) out[static_cast<int64_t>(m) * N + row0 + r] = from_f<XT>(v);
+    }
   }
 }
 
 bool qmv_q4_m1_supported(const QmmArgs& a) {
   // K in [1024, 16384]: one to eight 32-code chunks per lane per row
-  return a.transpose && a.M == 1 && a.mode == AFFINE && a.bits == 4 &&
-         (a.xdt == BF16 || a.xdt == F16) && a.K >= 1024 && a.K <= 16384;
+  // one matrix's codes below 4 GiB: row offsets are 32-bit
+  // M x rows share each unpacked weight chunk; their x pairs stay in
+  // registers, so M * chunks-per-lane is kept to 8.  Each extra row costs
+  // 16 dot2 per chunk, so from M = 4 the MFMA skinny kernel is faster.
+  const int cpl = ((a.K >> 5) + 63) / 64;
+  return a.transpose && a.M >= 1 && a.M <= 3 && a.M * cpl <= 8 && a.mode == AFFINE && a.bits == 4 &&
+         (a.xdt == BF16 || a.xdt == F16) && a.K >= 1024 && a.K <= 16384 &&
+         static_cast<int64_t>(a.N) * (a.K / 2) < (int64_t{1} << 32);
 }
 
 namespace {
+template <int XT, int RB, int CPL, int MR>
+void launch_mr(dim3 grid, const QmmArgs& a, const Q4Args& p, bool mapped, int64_t b0) {
+  if constexpr (MR * CPL > 8) return;  // excluded by qmv_q4_m1_supported
+  else if (mapped)
+    hipLaunchKernelGGL((qmv_q4_kernel<XT, RB, CPL, true, MR>), grid, dim3(64), 0, a.stream, p, a.bm, b0);
+  else
+    hipLaunchKernelGGL((qmv_q4_kernel<XT, RB, CPL, false, MR>), grid, dim3(64), 0, a.stream, p, a.bm, b0);
+}
+
 template <int XT, int RB, int CPL>
 hipError_t launch_ord(const QmmArgs& a) {
   const int64_t nrb = (a.N + RB - 1) / RB;
   if (nrb <= 0 || a.nbatch <= 0) return hipSuccess;
+  Q4Args p;
+  p.x = static_cast<const char*>(a.x);
+  p.w = reinterpret_cast<const char*>(a.w);
+  p.s = static_cast<const char*>(a.s);
+  p.b = static_cast<const char*>(a.b);
+  p.out = static_cast<char*>(a.out);
+  p.N = a.N;
+  p.K = a.K;
+  p.gshift = __builtin_ctz(a.gs);
+  p.pad = 0;
+  p.x_mat = a.x_mat * 2;
+  p.w_mat = a.w_mat * 4;
+  p.s_mat = a.s_mat * 2;
+  const bool mapped = a.bm.ndim != 0 || a.bm.lhs != nullptr || a.bm.rhs != nullptr;
   for (int64_t b0 = 0; b0 < a.nbatch; b0 += 65535) {
     const int64_t nb = a.nbatch - b0 < 65535 ? a.nbatch - b0 : 65535;
-    hipLaunchKernelGGL((qmv_q4_ord_kernel<XT, RB, CPL>),
-                       dim3(static_cast<unsigned>(nrb), static_cast<unsigned>(nb)), dim3(64), 0,
-                       a.stream, a, b0);
+    const dim3 grid(static_cast<unsigned>(nrb), static_cast<unsigned>(nb));
+    switch (a.M) {
+      case 1: launch_mr<XT, RB, CPL, 1>(grid, a, p, mapped, b0); break;
+      case 2: launch_mr<XT, RB, CPL, 2>(grid, a, p, mapped, b0); break;
+      default: launch_mr<XT, RB, CPL, 3>(grid, a, p, mapped, b0); break;
+    }
   }
   return hipGetLastError();
 }
 
 template <int XT, int CPL>
 hipError_t launch_ord_cpl(const QmmArgs& a) {
-  // rows per wave: 4 while that leaves >= 2048 waves, else fewer
+  // rows per wave (measured on MI355X): 2 from 4096 rows, 4 from 24576 rows
+  // (x and the per-chunk setup amortize over more rows once the grid is
+  // large), 1 below 4096 rows so small matrices still spread over the CUs
   const int64_t rows = a.N * a.nbatch;
-  int rb = rows >= 4 * 2048 ? 4 : rows >= 2 * 2048 ? 2 : 1;
+  int rb = rows >= 24576 ? 4 : rows >= 4096 ? 2 : 1;
   if (CPL >= 4 && rb > 2) rb = 2;
   switch (rb) {
     case 4: return launch_ord<XT, 4, CPL>(a);
