@@ -15,8 +15,6 @@
 // Reference op: mlx/src/ops.rs:695-727 with x = [B, 1, K] (one decode step
 // for B sequences, which mlx/src/generate/batch.rs:313-339 runs as B
 // separate M = 1 calls today).
-#include <stdlib.h>
-
 #include "launch.h"
 #include "mfma_common.h"
 
@@ -267,6 +265,229 @@ __global__ __launch_bounds__(64 * S) void qmm_skinny16_kernel(QmmArgs a, int nmt
     for (int w2 = 0; w2 < S; ++w2) v += red[(w2 * 32 + m) * 17 + n];
     if (m0 + m < M && n0 + n < N) out[static_cast<int64_t>(m0 + m) * N + n0 + n] = from_f<XT>(v);
   }
+}
+
+// ---------------------------------------------------------------------------
+// Factored affine 4-bit kernel for decode widths (transpose, K % 128 == 0).
+// The weights enter the MFMA undequantized: v_perm_b32 turns each nibble n
+// into the 16-bit value C + n (C = 128 bf16 / 1024 fp16, unit spacing) in the
+// pair order (n0,n4) (n2,n6) (n1,n5) (n3,n7), and x is permuted the same way.
+// With D = sum x (C + q) and X = sum x over one quantization group,
+//   sum x (s q + b) = s D + (b - C s) X,
+// so per 128-code block a lane spends 7 VALU per 8 codes on unpacking and two
+// FMAs per accumulator on the group scale, instead of a full dequantization.
+// A groups-per-block split keeps every MFMA's sum inside one group: the 16
+// A rows are (x row, group-in-block) pairs, so a 16-row m tile holds
+// RPT = 16 / GB x rows (GB = 128 / gs groups per block), and the A rows of
+// the other group are zero in each k slot.  X comes from the same MFMA with
+// an all-ones B.  A wave covers NT 16-row weight tiles (x pairs and X are
+// shared by them) for the blocks [pb, pe) of K; the S waves of a workgroup
+// split K and their partial sums meet in LDS.
+template <int XT, int NT, int MT, int GB, int S, int NB = 2>
+__global__ __launch_bounds__(64 * S) void qmm_skinny_fac_kernel(QmmArgs a) {
+  using XS = uint16_t;
+  constexpr int RPT = 16 / GB;
+  constexpr float CM = XT == BF16 ? 128.f : 1024.f;
+  constexpr uint32_t EB = XT == BF16 ? 0x43434343u : 0x64646464u;
+  constexpr uint32_t ONE2 = XT == BF16 ? 0x3f803f80u : 0x3c003c00u;
+  __shared__ float red[S * NT * MT * 256];
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int M = a.M, N = a.N, K = a.K;
+  const int n0 = blockIdx.x * 16 * NT;
+  const int64_t bb = blockIdx.y;
+  XS* out = static_cast<XS*>(a.out) + bb * static_cast<int64_t>(M) * N;
+  int64_t xb = 0, wb = 0;
+  if (a.bm.ndim != 0 || a.bm.lhs != nullptr || a.bm.rhs != nullptr) {
+    if (!map_batch(a.bm, bb, xb, wb)) {
+      for (int i = t; i < M * 16 * NT; i += 64 * S) {
+        const int m = i / (16 * NT), n = n0 + i % (16 * NT);
+        if (n < N) out[static_cast<int64_t>(m) * N + n] = from_f<XT>(__builtin_nanf(""));
+      }
+      return;
+    }
+  }
+  const char* x = reinterpret_cast<const char*>(static_cast<const XS*>(a.x) + xb * a.x_mat);
+  const char* w = reinterpret_cast<const char*>(a.w + wb * a.w_mat);
+  const char* sp = reinterpret_cast<const char*>(static_cast<const XS*>(a.s) + wb * a.s_mat);
+  const char* bp = reinterpret_cast<const char*>(static_cast<const XS*>(a.b) + wb * a.s_mat);
+  const int gshift = __builtin_ctz(a.gs);
+  const int64_t wrow = K / 2, srow = (K >> gshift) * 2, xrow = static_cast<int64_t>(K) * 2;
+  const int r = lane & 15, q = lane >> 4;
+  const int gq = (q * GB) >> 2;   // group (within the block) of this lane's k slot
+  // A rows: m tile i, row r -> x row i RPT + r % RPT, group r / RPT
+  const char* xr[MT];
+  bool xlive[MT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i) {
+    const int m = i * RPT + r % RPT;
+    xlive[i] = (r / RPT == gq) && m < M;
+    xr[i] = x + (xlive[i] ? m : 0) * xrow;
+  }
+  const char* wr[NT];
+  const char* sr[NT];
+  const char* br[NT];
+#pragma unroll
+  for (int tt = 0; tt < NT; ++tt) {
+    const int64_t n = min(n0 + 16 * tt + r, N - 1);
+    wr[tt] = w + n * wrow;
+    sr[tt] = sp + n * srow;
+    br[tt] = bp + n * srow;
+  }
+  const int P = K >> 7;
+  const int pb = (P * wave) / S, pe = (P * (wave + 1)) / S;
+
+  struct Blk {
+    g_u32x4_t xa[MT][4];
+    g_u32x4_t wv[NT];
+    XS sv[NT], bv[NT];
+  };
+  auto load = [&](int p, Blk& B) {
+    const int c = 4 * min(p, pe - 1) + q;   // chunk of this lane's k slot
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        B.xa[i][j] = *reinterpret_cast<const g_u32x4_t*>(xr[i] + c * 64 + 16 * j);
+    const int go = ((c * 32) >> gshift) * 2;
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) {
+      B.wv[tt] = __builtin_nontemporal_load(reinterpret_cast<const g_u32x4_t*>(wr[tt] + c * 16));
+      B.sv[tt] = *reinterpret_cast<const XS*>(sr[tt] + go);
+      B.bv[tt] = *reinterpret_cast<const XS*>(br[tt] + go);
+    }
+  };
+  f32x4_t Y[NT][MT];
+#pragma unroll
+  for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+    for (int i = 0; i < MT; ++i) Y[tt][i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const g_u32x4_t ones = {ONE2, ONE2, ONE2, ONE2};
+  auto compute = [&](const Blk& B) {
+    g_u32x4_t A[MT][4];
+    f32x4_t X[MT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        // (x0,x1) (x2,x3) (x4,x5) (x6,x7); rows of the other group (or past M)
+        // are zeroed here rather than by a predicated load, which would split
+        // the load stream into branches and serialize the waits
+        const g_u32x4_t v = xlive[i] ? B.xa[i][j] : g_u32x4_t{0, 0, 0, 0};
+        A[i][j] = g_u32x4_t{__builtin_amdgcn_perm(v.z, v.x, 0x05040100u), __builtin_amdgcn_perm(v.z, v.x, 0x07060302u),
+                            __builtin_amdgcn_perm(v.w, v.y, 0x05040100u), __builtin_amdgcn_perm(v.w, v.y, 0x07060302u)};
+      }
+      X[i] = mfma16x<XT>(A[i][0], ones, f32x4_t{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+      for (int j = 1; j < 4; ++j) X[i] = mfma16x<XT>(A[i][j], ones, X[i]);
+    }
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) {
+      const uint32_t wd[4] = {B.wv[tt].x, B.wv[tt].y, B.wv[tt].z, B.wv[tt].w};
+      g_u32x4_t Wp[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t lo = wd[j] & 0x0F0F0F0Fu, hi = (wd[j] >> 4) & 0x0F0F0F0Fu;
+        // pair order (n0,n4) (n1,n5) (n2,n6) (n3,n7), matching A above
+        Wp[j] = g_u32x4_t{__builtin_amdgcn_perm(EB, lo, 0x04020400u), __builtin_amdgcn_perm(EB, hi, 0x04020400u),
+                          __builtin_amdgcn_perm(EB, lo, 0x04030401u), __builtin_amdgcn_perm(EB, hi, 0x04030401u)};
+      }
+      const float s = to_f<XT>(B.sv[tt]), b = to_f<XT>(B.bv[tt]);
+      const float cb = fmaf(-CM, s, b);
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        f32x4_t D = mfma16x<XT>(A[i][0], Wp[0], f32x4_t{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+        for (int j = 1; j < 4; ++j) D = mfma16x<XT>(A[i][j], Wp[j], D);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) Y[tt][i][v] = fmaf(s, D[v], fmaf(cb, X[i][v], Y[tt][i][v]));
+      }
+    }
+  };
+  // NB blocks per round: all their loads are issued before any arithmetic
+  // (straight-line code, so each wait is exact); blocks past pe reload block
+  // pe - 1 with zero scale and bias and add nothing
+  for (int p0 = pb; p0 < pe; p0 += NB) {
+    Blk B[NB];
+#pragma unroll
+    for (int u = 0; u < NB; ++u) load(p0 + u, B[u]);
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      if (p0 + u >= pe) {
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt) B[u].sv[tt] = B[u].bv[tt] = 0;
+      }
+      compute(B[u]);
+    }
+  }
+  // lane holds Y[(m, group) = 4 q + v][n = r] of each (n tile, m tile)
+#pragma unroll
+  for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) red[((wave * NT + tt) * MT + i) * 256 + (4 * q + v) * 16 + r] = Y[tt][i][v];
+  __syncthreads();
+  for (int idx = t; idx < M * 16 * NT; idx += 64 * S) {
+    const int m = idx / (16 * NT), nn = idx % (16 * NT);
+    const int tt = nn >> 4, i = m / RPT, mr = m % RPT;
+    float acc = 0.f;
+#pragma unroll
+    for (int w2 = 0; w2 < S; ++w2)
+#pragma unroll
+      for (int g = 0; g < GB; ++g) acc += red[((w2 * NT + tt) * MT + i) * 256 + (mr + RPT * g) * 16 + (nn & 15)];
+    if (n0 + nn < N) out[static_cast<int64_t>(m) * N + n0 + nn] = from_f<XT>(acc);
+  }
+}
+
+namespace {
+template <int XT, int NT, int MT, int GB>
+hipError_t fac_launch_s(const QmmArgs& a, dim3 grid, int S) {
+  switch (S) {
+    case 8: hipLaunchKernelGGL((qmm_skinny_fac_kernel<XT, NT, MT, GB, 8>), grid, dim3(512), 0, a.stream, a); break;
+    case 4: hipLaunchKernelGGL((qmm_skinny_fac_kernel<XT, NT, MT, GB, 4>), grid, dim3(256), 0, a.stream, a); break;
+    case 2: hipLaunchKernelGGL((qmm_skinny_fac_kernel<XT, NT, MT, GB, 2>), grid, dim3(128), 0, a.stream, a); break;
+    default: hipLaunchKernelGGL((qmm_skinny_fac_kernel<XT, NT, MT, GB, 1>), grid, dim3(64), 0, a.stream, a); break;
+  }
+  return hipGetLastError();
+}
+template <int XT, int GB>
+hipError_t fac_launch_gb(const QmmArgs& a) {
+  constexpr int RPT = 16 / GB;
+  constexpr int NT = 2;
+  const int64_t nwg = (a.N + 16 * NT - 1) / (16 * NT);
+  if (nwg <= 0 || a.nbatch <= 0) return hipSuccess;
+  if (nwg > 0x7fffffffLL || a.nbatch > 65535) return hipErrorInvalidConfiguration;
+  const int P = a.K >> 7;
+  int S = 1;
+  while (S < 8 && P / (2 * S) >= 2 && nwg * a.nbatch * S < 4096) S *= 2;
+  const dim3 grid(static_cast<unsigned>(nwg), static_cast<unsigned>(a.nbatch));
+  if (a.M <= RPT) return fac_launch_s<XT, NT, 1, GB>(a, grid, S);
+  return fac_launch_s<XT, NT, 2, GB>(a, grid, S);
+}
+template <int XT>
+hipError_t fac_launch(const QmmArgs& a) {
+  switch (a.gs) {
+    case 32: return fac_launch_gb<XT, 4>(a);
+    case 64: return fac_launch_gb<XT, 2>(a);
+    default: return fac_launch_gb<XT, 1>(a);
+  }
+}
+}  // namespace
+
+bool qmm_skinny_fac_supported(const QmmArgs& a) {
+  if (!(a.transpose && a.mode == AFFINE && a.bits == 4 && (a.xdt == BF16 || a.xdt == F16) &&
+        a.K % 128 == 0 && a.K >= 128))
+    return false;
+  const int rpt = 16 / (128 / a.gs);   // x rows per m tile
+  // with fewer than 2048 waves (8 per 32-row tile pair) the split-K skinny
+  // kernel keeps more loads in flight
+  const int64_t waves = (a.N + 31) / 32 * 8 * a.nbatch;
+  return a.M >= 1 && a.M <= 2 * rpt && waves >= 2048;
+}
+
+hipError_t launch_qmm_skinny_fac(const QmmArgs& a) {
+  return a.xdt == BF16 ? fac_launch<BF16>(a) : fac_launch<F16>(a);
 }
 
 // ---------------------------------------------------------------------------

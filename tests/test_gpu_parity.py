@@ -164,6 +164,22 @@ def test_qmm_fp_modes(ops, mode, M, xdt):
 
 
 @pytest.mark.parametrize("xdt", ["bf16", "f16"])
+@pytest.mark.parametrize("N,K", [(200, 512), (8200, 1152)])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+@pytest.mark.parametrize("M", [4, 7, 8, 12, 16, 24, 32])
+def test_qmm_decode_widths_affine4(ops, M, gs, N, K, xdt):
+    # decode batch widths of the 4-bit path.  N = 8200 (ragged 32-row tile)
+    # is wide enough for the factored MFMA kernel (M up to two m tiles of
+    # 16 * gs / 128 rows, K % 128 == 0; K = 1152 has an odd block count for
+    # the split-K tail); N = 200 takes the split-K skinny kernel
+    if N > 1000 and xdt == "f16" and M not in (8, 16):
+        pytest.skip("f16 wide cases: M = 8, 16 cover the f16 magic constant")
+    rng = np.random.default_rng(M * 1000 + gs + K)
+    got, ref = _qmm_case(ops, rng, M, N, K, xdt, bits=4, gs=gs)
+    assert rel_err(got, ref) <= TOL[xdt]
+
+
+@pytest.mark.parametrize("xdt", ["bf16", "f16"])
 @pytest.mark.parametrize("M,N,K", [(100, 320, 1024), (300, 512, 256), (257, 96, 640), (520, 256, 1536)])
 @pytest.mark.parametrize("mode,bits,gs", [("affine", 4, 64), ("affine", 4, 32), ("affine", 4, 128),
                                           ("affine", 8, 64), ("affine", 3, 64), ("mxfp4", 4, 32),
