@@ -154,37 +154,90 @@ def bench_prefill(ops, steps, warmup, M=2048, N=14336, K=4096):
 
 def bench_moe(ops, Ts=(1, 64, 512), reps=10):
     """Qwen3.5-MoE-style gather_qmm: 256 experts, top-8 of softmax(N(0,1)
-    logits); gate 2048 -> 512 (q4 gs64, bf16).  GB/s counts the bytes of the
-    experts the sampled routing touches (plus x and out)."""
+    logits); gate (and up) 2048 -> 512 and down 512 -> 2048, q4 gs64, bf16.
+    GB/s counts the bytes of the experts the sampled routing touches (plus x
+    and out)."""
     E, H, I, k = 256, 2048, 512, 8
     gen = torch.Generator(device="cuda").manual_seed(3)
-    w = torch.randint(-2**31, 2**31 - 1, (E, I, H // 8), generator=gen, device="cuda",
-                      dtype=torch.int32).view(torch.uint32)
-    s = (torch.rand((E, I, H // 64), generator=gen, device="cuda") * 0.004 + 0.002).to(torch.bfloat16)
-    b = (torch.randn((E, I, H // 64), generator=gen, device="cuda") * 0.02).to(torch.bfloat16)
-    per_expert = I * H // 2 + 2 * I * (H // 64) * 2
+
+    def stack(n, kk):
+        w = torch.randint(-2**31, 2**31 - 1, (E, n, kk // 8), generator=gen, device="cuda",
+                          dtype=torch.int32).view(torch.uint32)
+        s = (torch.rand((E, n, kk // 64), generator=gen, device="cuda") * 0.004 + 0.002).to(torch.bfloat16)
+        b = (torch.randn((E, n, kk // 64), generator=gen, device="cuda") * 0.02).to(torch.bfloat16)
+        return w, s, b
+
+    gate, down = stack(I, H), stack(H, I)
+    per_expert = I * H // 2 + 2 * I * (H // 64) * 2   # one projection's bytes
     stream = torch.cuda.current_stream()
     out = {}
     for T in Ts:
         logits = torch.randn((T, E), generator=gen, device="cuda")
         idx = torch.topk(torch.softmax(logits, -1), k, dim=-1).indices.to(torch.int32)
         x = torch.randn((T, H), generator=gen, device="cuda").to(torch.bfloat16)
+        h = torch.randn((T * k, 1, I), generator=gen, device="cuda").to(torch.bfloat16)
         uniq = int(torch.unique(idx).numel())
         if T == 1:
-            xin, rhs, srt = x.view(T, 1, 1, H), idx, False
+            xin, hin, rhs, srt = x.view(T, 1, 1, H), h.view(T, k, 1, I), idx, False
         else:
             flat = idx.view(-1)
             order = torch.argsort(flat, stable=True)
-            xin, rhs, srt = x[order // k].view(T * k, 1, H).contiguous(), flat[order].contiguous(), True
-        fn = lambda: ops.gather_qmm(xin, w, s, b, None, rhs, True, 64, 4, "affine", srt)  # noqa: E731
-        fn()
-        torch.cuda.synchronize()
-        dt = time_launches(fn, reps, stream)
-        nbytes = uniq * per_expert + T * H * 2 + T * k * I * 2
-        out[str(T)] = {"unique_experts": uniq, "us": round(dt * 1e6, 2),
-                       "gbs": round(nbytes / dt / 1e9, 1),
-                       "tflops": round(2.0 * T * k * I * H / dt / 1e12, 2),
-                       "path": "sorted grouped" if srt else "per-token"}
+            xin, hin = x[order // k].view(T * k, 1, H).contiguous(), h
+            rhs, srt = flat[order].contiguous(), True
+        res = {"unique_experts": uniq, "path": "sorted grouped" if srt else "per-token"}
+        for name, (w, s, b), inp, n_out, kk in (("gate", gate, xin, I, H), ("down", down, hin, H, I)):
+            fn = lambda: ops.gather_qmm(inp, w, s, b, None, rhs, True, 64, 4, "affine", srt)  # noqa: E731
+            fn()
+            torch.cuda.synchronize()
+            dt = time_launches(fn, reps, stream)
+            nbytes = uniq * per_expert + T * k * (kk + n_out) * 2
+            res[name] = {"us": round(dt * 1e6, 2), "gbs": round(nbytes / dt / 1e9, 1),
+                         "tflops": round(2.0 * T * k * n_out * kk / dt / 1e12, 2)}
+        out[str(T)] = res
+    return out
+
+
+def graph_time(fn, n):
+    """Average device time of fn() over n calls captured in one HIP graph."""
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(n):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    g.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) * 1e-3 / n
+
+
+def bench_mode_sweep(ops, K=4096, N=4096, Ms=(1, 256), n=20):
+    """Mode / bit-width sweep at K = N = 4096: weights ~N(0, 0.02) quantized by
+    the library's own quantize for each mode, bf16 x; M = 1 reports weight GB/s,
+    M = 256 TFLOP/s."""
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    wf = (torch.randn((N, K), generator=gen, device="cuda") * 0.02).to(torch.bfloat16)
+    cases = [("affine", b, g) for b in (2, 3, 4, 6, 8) for g in (32, 64, 128)]
+    cases += [("mxfp4", 4, 32), ("mxfp8", 8, 32), ("nvfp4", 4, 16)]
+    out = {}
+    for mode, bits, gs in cases:
+        aff = mode == "affine"
+        wq, sq, bq = ops.quantize(wf, gs if aff else None, bits if aff else None, mode)
+        wbytes = wq.numel() * 4 + sq.numel() * sq.element_size() * (2 if aff else 1)
+        row = {}
+        for M in Ms:
+            x = torch.randn((M, K), generator=gen, device="cuda").to(torch.bfloat16)
+            fn = lambda: ops.quantized_matmul(x, wq, sq, bq, True, gs if aff else None,  # noqa: E731
+                                              bits if aff else None, mode)
+            dt = graph_time(fn, n)
+            row[str(M)] = ({"us": round(dt * 1e6, 2), "gbs": round(wbytes / dt / 1e9, 1)} if M == 1
+                           else {"us": round(dt * 1e6, 2), "tflops": round(2.0 * M * N * K / dt / 1e12, 1)})
+        out[f"{mode}{bits}" + (f"_gs{gs}" if aff else "")] = row
     return out
 
 
@@ -269,6 +322,8 @@ def run_only(ops, args):
         return {"only": "prefill", **{k: round(v, 3) for k, v in r.items()}}
     if args.only == "moe":
         return {"only": "moe", **bench_moe(ops)}
+    if args.only == "sweep":
+        return {"only": "sweep", **bench_mode_sweep(ops)}
     nbytes = 256 << 20
     a = torch.empty(nbytes // 4, dtype=torch.int32, device="cuda").fill_(1)
     b = torch.empty_like(a)
@@ -295,8 +350,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-llama", action="store_true")
+    ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--only", choices=["gemv", "prefill", "moe", "copy"], default=None,
+    ap.add_argument("--only", choices=["gemv", "prefill", "moe", "sweep", "copy"], default=None,
                     help="run one workload (for rocprofv3 kernel-trace / counter passes)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -316,6 +372,7 @@ def main():
     prefill = bench_prefill(ops, args.steps, args.warmup)
     prefill_down = bench_prefill(ops, args.steps, args.warmup, N=4096, K=14336)
     moe = bench_moe(ops)
+    sweep = None if args.no_sweep else bench_mode_sweep(ops)
     llama = None if args.no_llama else bench_llama_decode(ops)
     tr = load_traffic()
     traffic = tr.get("gemv_q4_gs64_k4096_n14336_m1", {}).get("traffic_bytes")
@@ -354,6 +411,8 @@ def main():
                     "down_proj_K14336_N4096_tflops": round(prefill_down["tflops"], 2)},
         "moe_gather_qmm": moe,
     }
+    if sweep is not None:
+        line["mode_sweep_k4096_n4096"] = sweep
     if llama is not None:
         line["llama3_8b_decode"] = llama
     if not args.no_cpu:
