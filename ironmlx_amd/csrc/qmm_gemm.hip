@@ -16,6 +16,7 @@
 
 #include <stdlib.h>
 
+#include <algorithm>
 #include <atomic>
 
 #include <type_traits>
@@ -572,37 +573,47 @@ __device__ __forceinline__ void tile_of(int bid, int ntm, int ntn, int& tm, int&
   tn = r / gsz;
 }
 
-template <int XT, int MODE, int BITS, int WD, int NCB, int RB>
-__global__ __launch_bounds__(64 * (8 / RB) * (8 / NCB), 1) void qmm_gemm_wr_kernel(QmmArgs a, int ntm, int ntn) {
+template <int XT, int MODE, int BITS, int WD, int TM, int TN>
+__global__ __launch_bounds__(2 * TN, 1) void qmm_gemm_wr_kernel(QmmArgs a, int ntm, int ntn, float* part) {
   static_assert(BITS == 4 || BITS == 8, "register-B kernel takes 4- and 8-bit codes");
   static_assert(WD % 2 == 0 && WD >= 4, "B double buffer alternates with the x slot");
   using XS = uint16_t;
   using CF = WrCfg<BITS>;
   constexpr bool AFF = MODE == AFFINE;
-  // waves: NWN across N (32 NCB columns each) x 8 / RB across M (32 RB rows each)
-  constexpr int NWN = 8 / NCB;
-  constexpr int NW = NWN * (8 / RB);
-  constexpr int NT = 64 * NW;
-  constexpr int XI = 16 / NW;           // x / W-chunk DMA instructions per wave
-  constexpr int SI = AFF ? 8 / NW : (NW >= 4 ? 1 : 4 / NW);  // scale-chunk instructions (waves < SW)
-  constexpr int SW = AFF ? NW : (NW >= 4 ? 4 : NW);
+  // tile TM x TN; wave w owns the TM x 32 column strip [32 w, 32 w + 32)
+  constexpr int NW = TN / 32, NT = 64 * NW, RB = TM / 32, NCB = 1;
+  constexpr int XI = TM / 16 / NW;      // x DMA instructions per wave (16 rows each)
+  constexpr int WI = 2;                 // W-chunk DMA instructions per wave (TN / 16 over NW)
+  constexpr int SQ = (TN / 64) * (AFF ? 2 : 1);  // scale(+bias)-chunk instructions
+  constexpr int SW = SQ < NW ? SQ : NW;          // waves issuing them, SI each
+  constexpr int SI = SQ / SW;
+  static_assert(XI >= 1 && XI * 16 * NW == TM && SI * SW == SQ, "tile / wave split");
   constexpr int GPC = AFF ? 8 : 16;  // groups per 16-byte scale chunk row
+  constexpr int XSTAGE = TM * DBK * 2;  // bytes of one x stage
+  constexpr int WSLOT = TN * 64;        // bytes of one W chunk slot
   extern __shared__ __attribute__((aligned(16))) uint16_t glds[];
   const int t = threadIdx.x, lane = t & 63, h = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);  // uniform: keeps DMA counts scalar
-  const int wn = wave % NWN, wm = wave / NWN;
+  const int wn = wave, wm = 0;
   const int M = a.M, N = a.N, K = a.K;
   int tm, tn;
   tile_of<4>(blockIdx.x, ntm, ntn, tm, tn);
-  const int m0 = tm * GBM, n0 = tn * GBN;
+  const int m0 = tm * TM, n0 = tn * TN;
+  // split K: this workgroup takes [kbeg, kbeg + klen); with more than one
+  // split the fp32 partial tile goes to part[z] and a second pass sums them
+  const int KSPL = gridDim.z, kz = blockIdx.z;
+  const int klen = K / KSPL, kbeg = kz * klen;
   const int64_t bb = blockIdx.y;
   XS* out = static_cast<XS*>(a.out) + bb * static_cast<int64_t>(M) * N;
   int64_t xb = 0, wb = 0;
   if (a.bm.ndim != 0 || a.bm.lhs != nullptr || a.bm.rhs != nullptr) {
     if (!map_batch(a.bm, bb, xb, wb)) {
-      for (int i = t; i < GBM * GBN; i += NT) {
-        const int r = m0 + i / GBN, c = n0 + i % GBN;
-        if (r < M && c < N) out[static_cast<int64_t>(r) * N + c] = from_f<XT>(__builtin_nanf(""));
+      for (int i = t; i < TM * TN; i += NT) {
+        const int r = m0 + i / TN, c = n0 + i % TN;
+        if (r < M && c < N) {
+          if (KSPL == 1) out[static_cast<int64_t>(r) * N + c] = from_f<XT>(__builtin_nanf(""));
+          else part[((static_cast<int64_t>(kz) * gridDim.y + bb) * M + r) * N + c] = __builtin_nanf("");
+        }
       }
       return;
     }
@@ -618,16 +629,16 @@ __global__ __launch_bounds__(64 * (8 / RB) * (8 / NCB), 1) void qmm_gemm_wr_kern
 
   // LDS map (bytes from glds): x ring (WD) | W chunk ring (WSL) | scale ring (2) | bias ring (2)
   constexpr int XR = 0;
-  constexpr int WR = XR + WD * DA_STAGE * 2;
-  constexpr int SR = WR + CF::WSL * CF::WSLOT;
-  constexpr int SSLOT = GBN * 16;
+  constexpr int WR = XR + WD * XSTAGE;
+  constexpr int SR = WR + CF::WSL * WSLOT;
+  constexpr int SSLOT = TN * 16;
   constexpr int BR = SR + 2 * SSLOT;
   char* lb = reinterpret_cast<char*>(glds);
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(lb));
 
   // ---- DMA: wave-uniform bases (SGPRs, advanced per step) + per-lane 32-bit
   // offsets within the tile, and wave-uniform LDS destinations
-  const char* xtile = reinterpret_cast<const char*>(x + static_cast<int64_t>(m0) * K);
+  const char* xtile = reinterpret_cast<const char*>(x + static_cast<int64_t>(m0) * K + kbeg);
   uint32_t xoff[XI], xdst_s[XI];
 #pragma unroll
   for (int i = 0; i < XI; ++i) {
@@ -637,32 +648,35 @@ __global__ __launch_bounds__(64 * (8 / RB) * (8 / NCB), 1) void qmm_gemm_wr_kern
     xoff[i] = static_cast<uint32_t>((min(m0 + row, M - 1) - m0) * K * 2 + g * 16);
     xdst_s[i] = __builtin_amdgcn_readfirstlane(lds0 + XR + rbase * DBK * 2);
   }
-  // W chunk: 256 rows x 4 granules = 16 instructions; stored granule p of
-  // row r holds logical granule p ^ f(r)
-  const char* wtile = w + static_cast<int64_t>(n0) * wrow;
-  uint32_t woff[XI], wdst_s[XI];
+  // W chunk: TN rows x 4 granules = TN / 16 instructions; stored granule p
+  // of row r holds logical granule p ^ f(r)
+  const char* wtile = w + static_cast<int64_t>(n0) * wrow + static_cast<int64_t>(kbeg) * BITS / 8;
+  uint32_t woff[WI], wdst_s[WI];
 #pragma unroll
-  for (int i = 0; i < XI; ++i) {
+  for (int i = 0; i < WI; ++i) {
     const int j = wave + NW * i;
     const int row = j * 16 + (lane >> 2);
     const int g = ((lane & 3) ^ dswzf(row)) & 3;
     woff[i] = static_cast<uint32_t>((min(n0 + row, N - 1) - n0) * wrow + g * 16);
     wdst_s[i] = __builtin_amdgcn_readfirstlane(lds0 + WR + j * 1024);
   }
-  // scale chunk: 64 rows x 16 B per instruction; 4 instructions of scales
-  // (+ 4 of biases), instruction q = wave + NW i on waves < SW
+  // scale chunk: 64 rows x 16 B per instruction; TN / 64 instructions of
+  // scales (+ as many of biases), instruction q = wave + NW i on waves < SW
+  constexpr int SQR = TN / 64;
   const int my_s = wave < SW ? SI : 0;
+  const int gshift = __builtin_ctz(gs);
   const char* stile[SI];
   uint32_t soff[SI], sdst_s[SI];
 #pragma unroll
   for (int i = 0; i < SI; ++i) {
-    const int q = min(wave + NW * i, AFF ? 7 : 3);
-    const int srow = min(n0 + (q & 3) * 64 + lane, N - 1);
-    stile[i] = ((AFF && q >= 4) ? bbase : sbase) + static_cast<int64_t>(n0) * G * ssz;
+    const int q = min(wave + NW * i, SQ - 1);
+    const bool isb = AFF && q >= SQR;
+    const int qr = isb ? q - SQR : q;
+    const int srow = min(n0 + qr * 64 + lane, N - 1);
+    stile[i] = (isb ? bbase : sbase) + (static_cast<int64_t>(n0) * G + (kbeg >> gshift)) * ssz;
     soff[i] = static_cast<uint32_t>((srow - n0) * G * ssz);
-    sdst_s[i] = __builtin_amdgcn_readfirstlane(lds0 + (AFF && q >= 4 ? BR : SR) + (q & 3) * 1024);
+    sdst_s[i] = __builtin_amdgcn_readfirstlane(lds0 + (isb ? BR : SR) + qr * 1024);
   }
-  const int gshift = __builtin_ctz(gs);
   // steps per scale chunk (P = GPC * gs / 32 >= 8)
   const int pshift = __builtin_ctz(GPC) + gshift - 5;
   constexpr int WCS = BITS == 4 ? 2 : 1;  // log2(WC)
@@ -675,12 +689,12 @@ __global__ __launch_bounds__(64 * (8 / RB) * (8 / NCB), 1) void qmm_gemm_wr_kern
     const int k0 = j * DBK;
     const char* xk = xtile + k0 * 2;
 #pragma unroll
-    for (int i = 0; i < XI; ++i) dma_x4s(xoff[i], xk, xdst_s[i] + SL * DA_STAGE * 2);
+    for (int i = 0; i < XI; ++i) dma_x4s(xoff[i], xk, xdst_s[i] + SL * XSTAGE);
     if constexpr (WCH) {
-      const uint32_t wsl = ((j >> WCS) % CF::WSL) * CF::WSLOT;
+      const uint32_t wsl = ((j >> WCS) % CF::WSL) * WSLOT;
       const char* wk = wtile + (k0 >> 5) * CF::STEP_B;
 #pragma unroll
-      for (int i = 0; i < XI; ++i) dma_x4s(woff[i], wk, wdst_s[i] + wsl);
+      for (int i = 0; i < WI; ++i) dma_x4s(woff[i], wk, wdst_s[i] + wsl);
     }
     if ((j & ((1 << pshift) - 1)) == 0 && my_s) {
       const int g0 = k0 >> gshift;
@@ -694,7 +708,7 @@ __global__ __launch_bounds__(64 * (8 / RB) * (8 / NCB), 1) void qmm_gemm_wr_kern
     const int cn = 32 * (NCB * wn + cb) + (lane & 31);
     const int wsw = dswzf(cn);
     const int g = (ks * DBK) >> gshift;
-    const char* ch = lb + WR + ((ks >> WCS) % CF::WSL) * CF::WSLOT;
+    const char* ch = lb + WR + ((ks >> WCS) % CF::WSL) * WSLOT;
     const char* sc = lb + ((ks >> pshift) & 1) * SSLOT + cn * 16;
     const int gi = g & (GPC - 1);
     float sv[2], bv = 0.f;
@@ -769,7 +783,7 @@ __global__ __launch_bounds__(64 * (8 / RB) * (8 / NCB), 1) void qmm_gemm_wr_kern
   // its last use, so the next step starts with its operands in flight.
   auto mfma_step = [&](const g_u32x4_t (&bf)[NCB][2], g_u32x4_t (&af)[2][RB], auto sn_c) {
     constexpr int SN = decltype(sn_c)::value;
-    const char* An = lb + XR + SN * DA_STAGE * 2;
+    const char* An = lb + XR + SN * XSTAGE;
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
@@ -786,7 +800,7 @@ __global__ __launch_bounds__(64 * (8 / RB) * (8 / NCB), 1) void qmm_gemm_wr_kern
   // DMAs of steps ks+3 .. ks+WD-1 may still be in flight.  W / scale chunk
   // slots are refilled only after every reader of their previous chunk has
   // passed a barrier ((WSL - 1) WC > WD - 3 and P > WD - 3 steps).
-  const int nk = K / DBK;
+  const int nk = klen / DBK;
   g_u32x4_t bq[2][NCB][2], af[2][RB];
   static_for<0, WD - 1>([&](auto s_c) {
     constexpr int J = decltype(s_c)::value;
@@ -797,7 +811,7 @@ __global__ __launch_bounds__(64 * (8 / RB) * (8 / NCB), 1) void qmm_gemm_wr_kern
     if (nk >= WD - 1) {
       constexpr int nx = [] {
         int n = 0;
-        for (int j = 2; j <= WD - 2; ++j) n += XI + (j % CF::WC == 0 ? XI : 0);
+        for (int j = 2; j <= WD - 2; ++j) n += XI + (j % CF::WC == 0 ? WI : 0);
         return n;
       }();
       wait_vmc<nx>();   // scale chunks are issued at j = 0 only within 0 .. WD-2 (P >= 8)
@@ -839,7 +853,7 @@ __global__ __launch_bounds__(64 * (8 / RB) * (8 / NCB), 1) void qmm_gemm_wr_kern
             // DMAs of steps ks+3 .. ks+WD-1 may stay in flight
             constexpr int nx = [] {
               int n = 0;
-              for (int j = S + 3; j <= S + WD - 1; ++j) n += XI + (j % CF::WC == 0 ? XI : 0);
+              for (int j = S + 3; j <= S + WD - 1; ++j) n += XI + (j % CF::WC == 0 ? WI : 0);
               return n;
             }();
             if (my_s && ((ks + WD - 1) & pmask) <= WD - 4) wait_vmc<nx + SI>();
@@ -855,6 +869,20 @@ __global__ __launch_bounds__(64 * (8 / RB) * (8 / NCB), 1) void qmm_gemm_wr_kern
     });
   }
 
+  if (KSPL > 1) {
+    float* pt = part + (static_cast<int64_t>(kz) * gridDim.y + bb) * M * N;
+    const int col = n0 + 32 * wn + (lane & 31);
+    if (col < N) {
+#pragma unroll
+      for (int i = 0; i < RB; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int row = m0 + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+          if (row < M) pt[static_cast<int64_t>(row) * N + col] = acc[i][0][v];
+        }
+    }
+    return;
+  }
   if (m0 + 32 * RB * (wm + 1) <= M) {
     // full row tile: wave-uniform row bases (SGPRs) + one 32-bit lane offset
 #pragma unroll
@@ -890,8 +918,31 @@ __global__ __launch_bounds__(64 * (8 / RB) * (8 / NCB), 1) void qmm_gemm_wr_kern
 }
 
 template <int BITS>
-constexpr size_t wr_lds_bytes(int wd) {
-  return static_cast<size_t>(wd) * DA_STAGE * 2 + WrCfg<BITS>::WSL * WrCfg<BITS>::WSLOT + 4 * GBN * 16;
+constexpr size_t wr_lds_bytes(int wd, int tm, int tn) {
+  return static_cast<size_t>(wd) * tm * DBK * 2 + WrCfg<BITS>::WSL * tn * 64 + 4 * tn * 16;
+}
+
+// sum of the split-K fp32 partials -> x's 16-bit type
+template <int XT>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* part, uint16_t* out, int64_t n,
+                                                            int ks) {
+  const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
+  if (i >= n) return;
+  if (i + 4 <= n) {
+    float4 acc = *reinterpret_cast<const float4*>(part + i);
+    for (int z = 1; z < ks; ++z) {
+      const float4 v = *reinterpret_cast<const float4*>(part + z * n + i);
+      acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+    }
+    out[i] = from_f<XT>(acc.x); out[i + 1] = from_f<XT>(acc.y);
+    out[i + 2] = from_f<XT>(acc.z); out[i + 3] = from_f<XT>(acc.w);
+  } else {
+    for (int64_t j = i; j < n; ++j) {
+      float acc = part[j];
+      for (int z = 1; z < ks; ++z) acc += part[z * n + j];
+      out[j] = from_f<XT>(acc);
+    }
+  }
 }
 
 template <int BITS, int MODE>
@@ -920,6 +971,54 @@ hipError_t set_lds_once(size_t bytes) {
   return e;
 }
 
+template <int XT, int MODE, int BITS, int TM, int TN>
+hipError_t wr_launch_tile(const QmmArgs& a, int ks, float* part) {
+  constexpr int WD = 6;
+  const int ntm = (a.M + TM - 1) / TM, ntn = (a.N + TN - 1) / TN;
+  const int64_t nblk = static_cast<int64_t>(ntm) * ntn;
+  if (nblk > 0x7fffffffLL || a.nbatch > 65535) return hipErrorInvalidConfiguration;
+  constexpr auto kern = qmm_gemm_wr_kernel<XT, MODE, BITS, WD, TM, TN>;
+  constexpr size_t lds = wr_lds_bytes<BITS>(WD, TM, TN);
+  hipError_t e = set_lds_once<kern>(lds);
+  if (e != hipSuccess) return e;
+  const dim3 grid(static_cast<unsigned>(nblk), static_cast<unsigned>(a.nbatch), static_cast<unsigned>(ks));
+  hipLaunchKernelGGL(kern, grid, dim3(2 * TN), lds, a.stream, a, ntm, ntn, part);
+  return hipGetLastError();
+}
+
+// Tile / split choice for the register-B kernel: 256 x 256 tiles while they
+// give most CUs a tile; otherwise 128 x 128 tiles with K split over enough
+// workgroups to fill the GPU.  Split partials are fp32 in a stream-ordered
+// workspace (hipMallocAsync / hipFreeAsync) summed in a fixed order by
+// splitk_reduce_kernel, so results do not depend on scheduling.
+template <int XT, int MODE, int BITS>
+hipError_t wr_launch(const QmmArgs& a, int G) {
+  const int64_t big = ((a.M + 255) / 256) * ((a.N + 255) / 256) * a.nbatch;
+  if (big >= 192) return wr_launch_tile<XT, MODE, BITS, 256, 256>(a, 1, nullptr);
+  const int64_t small = ((a.M + 127) / 128) * ((a.N + 127) / 128) * a.nbatch;
+  // each split keeps whole scale chunks (8 or 16 groups) and 128-code W chunks
+  const int gs = MODE == AFFINE ? a.gs : ModeInfo<MODE>::GS;
+  const int span = std::max(128, (MODE == AFFINE ? 8 : 16) * gs);
+  int ks = 1;
+  while (small * ks < 256 && ks < 16 && a.K % (span * ks * 2) == 0 && a.K / (ks * 2) >= 512) ks *= 2;
+  (void)G;
+  if (ks == 1) return wr_launch_tile<XT, MODE, BITS, 128, 128>(a, 1, nullptr);
+  const int64_t n = static_cast<int64_t>(a.nbatch) * a.M * a.N;
+  float* part = nullptr;
+  hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&part), static_cast<size_t>(n) * ks * sizeof(float),
+                                a.stream);
+  if (e != hipSuccess) return e;
+  e = wr_launch_tile<XT, MODE, BITS, 128, 128>(a, ks, part);
+  if (e == hipSuccess) {
+    const int64_t nb = (n + 1023) / 1024;
+    hipLaunchKernelGGL(splitk_reduce_kernel<XT>, dim3(static_cast<unsigned>(nb)), dim3(256), 0, a.stream, part,
+                       static_cast<uint16_t*>(a.out), n, ks);
+    e = hipGetLastError();
+  }
+  const hipError_t f = hipFreeAsync(part, a.stream);
+  return e != hipSuccess ? e : f;
+}
+
 template <int XT, int MODE, int BITS>
 hipError_t gemm_launch_t(const QmmArgs& a) {
   const int ntm = (a.M + GBM - 1) / GBM, ntn = (a.N + GBN - 1) / GBN;
@@ -934,13 +1033,7 @@ hipError_t gemm_launch_t(const QmmArgs& a) {
   const bool wr_ok = dma_ok && (BITS == 4 || BITS == 8) && a.K % (32 * (BITS == 4 ? 4 : 2)) == 0 &&
                      G % GPC == 0;
   if (wr_ok) {
-    if constexpr (BITS == 4 || BITS == 8) {
-      constexpr auto kern = qmm_gemm_wr_kernel<XT, MODE, BITS, WD, 1, 8>;
-      constexpr size_t lds = wr_lds_bytes<BITS>(WD);
-      hipError_t e = set_lds_once<kern>(lds);
-      if (e != hipSuccess) return e;
-      hipLaunchKernelGGL(kern, grid, dim3(512), lds, a.stream, a, ntm, ntn);
-    }
+    if constexpr (BITS == 4 || BITS == 8) return wr_launch<XT, MODE, BITS>(a, G);
   } else if (dma_ok) {
     constexpr auto kern = qmm_gemm_dma8_kernel<XT, MODE, BITS>;
     constexpr size_t lds = dma_lds_bytes<BITS, MODE>();

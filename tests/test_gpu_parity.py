@@ -164,6 +164,19 @@ def test_qmm_fp_modes(ops, mode, M, xdt):
 
 
 @pytest.mark.parametrize("xdt", ["bf16", "f16"])
+@pytest.mark.parametrize("M", [128, 256])
+@pytest.mark.parametrize("mode,bits,gs", [("affine", 4, 64), ("affine", 8, 32), ("mxfp4", 4, 32),
+                                          ("nvfp4", 4, 16), ("mxfp8", 8, 32)])
+def test_qmm_split_k_tiles(ops, mode, bits, gs, M, xdt):
+    # few output tiles (M <= 256, N = 1024): 128 x 128 tiles with K split
+    # over workgroups, fp32 partials summed in a second pass
+    rng = np.random.default_rng(M + bits + gs)
+    got, ref = _qmm_case(ops, rng, M, 1024, 4096, xdt, mode=mode, bits=bits, gs=gs)
+    tol = TOL if mode == "affine" else TOL_FP
+    assert rel_err(got, ref) <= tol[xdt]
+
+
+@pytest.mark.parametrize("xdt", ["bf16", "f16"])
 @pytest.mark.parametrize("N,K", [(200, 512), (8200, 1152)])
 @pytest.mark.parametrize("gs", [32, 64, 128])
 @pytest.mark.parametrize("M", [4, 7, 8, 12, 16, 24, 32])
