@@ -113,6 +113,37 @@ __device__ __forceinline__ void chunk_pairs(const u32x4_t& wv, uint32_t (&W)[16]
   }
 }
 
+// fp4 (e2m1) chunk -> 16 pairs in the same (n0,n4) (n2,n6) (n1,n5) (n3,n7)
+// order.  The 3-bit magnitude indexes an 8-byte table with v_perm_b32 (high
+// and low bytes of the 16-bit value {0, .5, 1, 1.5, 2, 3, 4, 6}); the sign bit
+// moves to bit 7 of the high byte.  Every value is exact in bf16 and fp16.
+template <int XT>
+__device__ __forceinline__ void fp4_pairs(const u32x4_t& wv, uint32_t (&W)[16]) {
+  // high bytes: bf16 00 3f 3f 3f 40 40 40 40, fp16 00 38 3c 3e 40 42 44 46
+  constexpr uint32_t H0 = XT == BF16 ? 0x3f3f3f00u : 0x3e3c3800u;
+  constexpr uint32_t H1 = XT == BF16 ? 0x40404040u : 0x46444240u;
+  // low bytes (bf16 only): 00 00 80 c0 00 40 80 c0
+  constexpr uint32_t L0 = 0xc0800000u, L1 = 0xc0804000u;
+  const uint32_t wd[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const uint32_t c = (half ? wd[q] >> 4 : wd[q]) & 0x0F0F0F0Fu;   // codes n(2i+half)
+      const uint32_t m = c & 0x07070707u;
+      const uint32_t hb = __builtin_amdgcn_perm(H1, H0, m) | ((c << 4) & 0x80808080u);
+      if constexpr (XT == BF16) {
+        const uint32_t lb = __builtin_amdgcn_perm(L1, L0, m);
+        W[4 * q + 2 * half + 0] = __builtin_amdgcn_perm(hb, lb, 0x06020400u);
+        W[4 * q + 2 * half + 1] = __builtin_amdgcn_perm(hb, lb, 0x07030501u);
+      } else {
+        W[4 * q + 2 * half + 0] = __builtin_amdgcn_perm(hb, hb, 0x060c040cu);
+        W[4 * q + 2 * half + 1] = __builtin_amdgcn_perm(hb, hb, 0x070c050cu);
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Single-pass kernel.  One wave per workgroup owns RB rows; lane l owns
 // chunks l, l+64, ... (CPL per row).  Every load is issued before any
@@ -132,7 +163,7 @@ struct Q4Args {
   int64_t x_mat, w_mat, s_mat;  // byte strides between batch elements
 };
 
-template <int XT, int RB, int CPL, bool MAPPED, int MR>
+template <int XT, int RB, int CPL, bool MAPPED, int MR, int MODE = AFFINE>
 __global__ __launch_bounds__(64) void qmv_q4_kernel(Q4Args p, BatchMap bm, int64_t batch0) {
   using XS = uint16_t;
   const int lane = threadIdx.x;
@@ -155,7 +186,9 @@ __global__ __launch_bounds__(64) void qmv_q4_kernel(Q4Args p, BatchMap bm, int64
   const char* bp = p.b + wi * p.s_mat;
   // bytes per row; one matrix's packed codes and scales stay below 4 GiB
   // (checked by the launcher), so row offsets are 32-bit scalar products
-  const uint32_t wrow = static_cast<uint32_t>(K) >> 1, srow = (static_cast<uint32_t>(K) >> p.gshift) * 2;
+  const uint32_t wrow = static_cast<uint32_t>(K) >> 1;
+  const uint32_t srow = MODE == AFFINE ? (static_cast<uint32_t>(K) >> p.gshift) * 2
+                                       : static_cast<uint32_t>(K) >> (MODE == MXFP4 ? 5 : 4);
   const uint32_t xrow = static_cast<uint32_t>(K) * 2;
 
   // per-lane byte offsets (32-bit) of each slot's chunk, x chunk and group
@@ -165,7 +198,9 @@ __global__ __launch_bounds__(64) void qmv_q4_kernel(Q4Args p, BatchMap bm, int64
     const uint32_t cidx = static_cast<uint32_t>(min(lane + 64 * j, C - 1));
     cw[j] = cidx << 4;
     cx[j] = cidx << 6;
-    cg[j] = ((cidx << 5) >> p.gshift) * 2;
+    // scale byte offset: affine 16-bit per group, MX one byte per chunk,
+    // NV two bytes (groups 2c, 2c+1) per chunk
+    cg[j] = MODE == AFFINE ? ((cidx << 5) >> p.gshift) * 2 : MODE == MXFP4 ? cidx : 2 * cidx;
   }
 
   // 1. x chunks (cache-resident) first
@@ -192,8 +227,14 @@ __global__ __launch_bounds__(64) void qmv_q4_kernel(Q4Args p, BatchMap bm, int64
       wv[r][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(wr + cw[j]));
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-      sr[r][j] = *reinterpret_cast<const XS*>(sr_ + cg[j]);
-      br[r][j] = *reinterpret_cast<const XS*>(br_ + cg[j]);
+      if constexpr (MODE == AFFINE) {
+        sr[r][j] = *reinterpret_cast<const XS*>(sr_ + cg[j]);
+        br[r][j] = *reinterpret_cast<const XS*>(br_ + cg[j]);
+      } else if constexpr (MODE == MXFP4) {
+        sr[r][j] = *reinterpret_cast<const uint8_t*>(sr_ + cg[j]);
+      } else {
+        sr[r][j] = *reinterpret_cast<const XS*>(sr_ + cg[j]);
+      }
     }
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -210,7 +251,19 @@ __global__ __launch_bounds__(64) void qmv_q4_kernel(Q4Args p, BatchMap bm, int64
         X[4 * i] = xv[m][j][i].x; X[4 * i + 1] = xv[m][j][i].y;
         X[4 * i + 2] = xv[m][j][i].z; X[4 * i + 3] = xv[m][j][i].w;
       }
-      make_pairs<XT>(X, P[m][j], xs[m][j]);
+      if constexpr (MODE == AFFINE) {
+        make_pairs<XT>(X, P[m][j], xs[m][j]);
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t A0 = X[4 * q], A1 = X[4 * q + 1], B0 = X[4 * q + 2], B1 = X[4 * q + 3];
+          P[m][j][4 * q + 0] = __builtin_amdgcn_perm(B0, A0, 0x05040100u);
+          P[m][j][4 * q + 1] = __builtin_amdgcn_perm(B1, A1, 0x05040100u);
+          P[m][j][4 * q + 2] = __builtin_amdgcn_perm(B0, A0, 0x07060302u);
+          P[m][j][4 * q + 3] = __builtin_amdgcn_perm(B1, A1, 0x07060302u);
+        }
+        xs[m][j] = 0.f;
+      }
       if (lane + 64 * j >= C) xs[m][j] = 0.f;  // masked slot contributes nothing
     }
   // 4. rows in load order
@@ -222,6 +275,23 @@ __global__ __launch_bounds__(64) void qmv_q4_kernel(Q4Args p, BatchMap bm, int64
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
       const bool live = lane + 64 * j < C;
+      if constexpr (MODE != AFFINE) {
+        uint32_t Wp[16];
+        fp4_pairs<XT>(wv[r][j], Wp);
+        float d0 = 0.f, d1 = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) d0 = dot2<XT>(Wp[i], P[0][j][i], d0);
+#pragma unroll
+        for (int i = 8; i < 16; ++i) d1 = dot2<XT>(Wp[i], P[0][j][i], d1);
+        if (!live) d0 = d1 = 0.f;
+        if constexpr (MODE == MXFP4) {
+          acc[0] = fmaf(fp_scale<MODE>(sr[r][j]), d0 + d1, acc[0]);
+        } else {
+          acc[0] = fmaf(fp_scale<MODE>(sr[r][j] & 0xffu), d0, acc[0]);
+          acc[0] = fmaf(fp_scale<MODE>(sr[r][j] >> 8), d1, acc[0]);
+        }
+        continue;
+      }
       const float s = to_f<XT>(sr[r][j]), b = to_f<XT>(br[r][j]);
       if constexpr (MR == 1) {
         float d = chunk_dot<XT>(wv[r][j], P[0][j]);
@@ -255,19 +325,21 @@ bool qmv_q4_m1_supported(const QmmArgs& a) {
   // registers, so M * chunks-per-lane is kept to 8.  Each extra row costs
   // 16 dot2 per chunk, so from M = 4 the MFMA skinny kernel is faster.
   const int cpl = ((a.K >> 5) + 63) / 64;
-  return a.transpose && a.M >= 1 && a.M <= 3 && a.M * cpl <= 8 && a.mode == AFFINE && a.bits == 4 &&
+  // mxfp4 / nvfp4 (e2m1 codes, one or two byte scales per chunk) at M = 1
+  const bool mode_ok = a.mode == AFFINE ? a.bits == 4 : (a.mode == MXFP4 || a.mode == NVFP4) && a.M == 1;
+  return a.transpose && a.M >= 1 && a.M <= 3 && a.M * cpl <= 8 && mode_ok &&
          (a.xdt == BF16 || a.xdt == F16) && a.K >= 1024 && a.K <= 16384 &&
          static_cast<int64_t>(a.N) * (a.K / 2) < (int64_t{1} << 32);
 }
 
 namespace {
-template <int XT, int RB, int CPL, int MR>
+template <int XT, int RB, int CPL, int MR, int MODE = AFFINE>
 void launch_mr(dim3 grid, const QmmArgs& a, const Q4Args& p, bool mapped, int64_t b0) {
   if constexpr (MR * CPL > 8) return;  // excluded by qmv_q4_m1_supported
   else if (mapped)
-    hipLaunchKernelGGL((qmv_q4_kernel<XT, RB, CPL, true, MR>), grid, dim3(64), 0, a.stream, p, a.bm, b0);
+    hipLaunchKernelGGL((qmv_q4_kernel<XT, RB, CPL, true, MR, MODE>), grid, dim3(64), 0, a.stream, p, a.bm, b0);
   else
-    hipLaunchKernelGGL((qmv_q4_kernel<XT, RB, CPL, false, MR>), grid, dim3(64), 0, a.stream, p, a.bm, b0);
+    hipLaunchKernelGGL((qmv_q4_kernel<XT, RB, CPL, false, MR, MODE>), grid, dim3(64), 0, a.stream, p, a.bm, b0);
 }
 
 template <int XT, int RB, int CPL>
@@ -282,7 +354,7 @@ hipError_t launch_ord(const QmmArgs& a) {
   p.out = static_cast<char*>(a.out);
   p.N = a.N;
   p.K = a.K;
-  p.gshift = __builtin_ctz(a.gs);
+  p.gshift = a.mode == AFFINE ? __builtin_ctz(a.gs) : 0;
   p.pad = 0;
   p.x_mat = a.x_mat * 2;
   p.w_mat = a.w_mat * 4;
@@ -291,6 +363,8 @@ hipError_t launch_ord(const QmmArgs& a) {
   for (int64_t b0 = 0; b0 < a.nbatch; b0 += 65535) {
     const int64_t nb = a.nbatch - b0 < 65535 ? a.nbatch - b0 : 65535;
     const dim3 grid(static_cast<unsigned>(nrb), static_cast<unsigned>(nb));
+    if (a.mode == MXFP4) { launch_mr<XT, RB, CPL, 1, MXFP4>(grid, a, p, mapped, b0); continue; }
+    if (a.mode == NVFP4) { launch_mr<XT, RB, CPL, 1, NVFP4>(grid, a, p, mapped, b0); continue; }
     switch (a.M) {
       case 1: launch_mr<XT, RB, CPL, 1>(grid, a, p, mapped, b0); break;
       case 2: launch_mr<XT, RB, CPL, 2>(grid, a, p, mapped, b0); break;

@@ -164,6 +164,17 @@ def test_qmm_fp_modes(ops, mode, M, xdt):
 
 
 @pytest.mark.parametrize("xdt", ["bf16", "f16"])
+@pytest.mark.parametrize("K", [1024, 4096, 14336])
+@pytest.mark.parametrize("mode", ["mxfp4", "nvfp4"])
+def test_qmv_fp4_gemv(ops, mode, K, xdt):
+    # M = 1 fp4 GEMV: e2m1 codes through the byte-table unpack, one (MX) or
+    # two (NV) byte scales per 32-code chunk
+    rng = np.random.default_rng(K + len(mode))
+    got, ref = _qmm_case(ops, rng, 1, 300, K, xdt, mode=mode)
+    assert rel_err(got, ref) <= TOL_FP[xdt]
+
+
+@pytest.mark.parametrize("xdt", ["bf16", "f16"])
 @pytest.mark.parametrize("M", [128, 256])
 @pytest.mark.parametrize("mode,bits,gs", [("affine", 4, 64), ("affine", 8, 32), ("mxfp4", 4, 32),
                                           ("nvfp4", 4, 16), ("mxfp8", 8, 32)])
