@@ -297,7 +297,7 @@ __device__ __forceinline__ void static_for(F&& f) {
 }
 
 template <int XT, int MODE, int BITS>
-__global__ __launch_bounds__(512, 1) void qmm_gemm_dma8_kernel(QmmArgs a, int ntm, int ntn) {
+__global__ __launch_bounds__(512, 1) void qmm_gemm_dma8_kernel(QmmArgs a, int ntm, int ntn, float* part) {
   using XS = uint16_t;
   using DC = DmaCounts<BITS, MODE>;
   constexpr bool AFF = MODE == AFFINE;
@@ -313,12 +313,19 @@ __global__ __launch_bounds__(512, 1) void qmm_gemm_dma8_kernel(QmmArgs a, int nt
   const int m0 = tm * GBM, n0 = tn * GBN;
   const int64_t bb = blockIdx.y;
   XS* out = static_cast<XS*>(a.out) + bb * static_cast<int64_t>(M) * N;
+  // split K as in the register-B kernel: [kbeg, kbeg + klen), fp32 partials
+  const int KSPL = gridDim.z, kz = blockIdx.z;
+  const int klen = K / KSPL, kbeg = kz * klen;
+  float* pt = part + (static_cast<int64_t>(kz) * gridDim.y + bb) * M * N;
   int64_t xb = 0, wb = 0;
   if (a.bm.ndim != 0 || a.bm.lhs != nullptr || a.bm.rhs != nullptr) {
     if (!map_batch(a.bm, bb, xb, wb)) {
       for (int i = t; i < GBM * GBN; i += 512) {
         const int r = m0 + i / GBN, c = n0 + i % GBN;
-        if (r < M && c < N) out[static_cast<int64_t>(r) * N + c] = from_f<XT>(__builtin_nanf(""));
+        if (r < M && c < N) {
+          if (KSPL == 1) out[static_cast<int64_t>(r) * N + c] = from_f<XT>(__builtin_nanf(""));
+          else pt[static_cast<int64_t>(r) * N + c] = __builtin_nanf("");
+        }
       }
       return;
     }
@@ -348,7 +355,7 @@ __global__ __launch_bounds__(512, 1) void qmm_gemm_dma8_kernel(QmmArgs a, int nt
     const int rbase = (wave + NW * i) * 16;
     const int row = rbase + (lane >> 2);
     const int g = ((lane & 3) ^ dswzf(row)) & 3;
-    xsrc[i] = x + static_cast<int64_t>(min(m0 + row, M - 1)) * K + g * 8;
+    xsrc[i] = x + static_cast<int64_t>(min(m0 + row, M - 1)) * K + kbeg + g * 8;
     xdst[i] = rbase * DBK * 2;
   }
   const int my_w = (WINSTR - wave + NW - 1) / NW;
@@ -367,11 +374,12 @@ __global__ __launch_bounds__(512, 1) void qmm_gemm_dma8_kernel(QmmArgs a, int nt
     const int j = min(wave + NW * jj, WINSTR - 1);
     const int idx = j * 64 + lane;
     const int row = idx / BITS, word = idx - row * BITS;
-    wsrc[jj] = w + min(n0 + row, N - 1) * wpr + word;
+    wsrc[jj] = w + min(n0 + row, N - 1) * wpr + static_cast<int64_t>(kbeg) * BITS / 32 + word;
     wdst_s[jj] = __builtin_amdgcn_readfirstlane(lds0 + WR + j * 256);
   }
   const int srow = min(n0 + (wave & 3) * 64 + lane, N - 1);
-  const char* ssrc = ((AFF && wave >= 4) ? bbase : sbase) + static_cast<int64_t>(srow) * G * (AFF ? 2 : 1);
+  const char* ssrc = ((AFF && wave >= 4) ? bbase : sbase) +
+                     (static_cast<int64_t>(srow) * G + (kbeg >> gshift)) * (AFF ? 2 : 1);
   const uint32_t sdst_s = __builtin_amdgcn_readfirstlane(lds0 + (AFF && wave >= 4 ? BR : SR) + (wave & 3) * 256);
 
   auto issue = [&](int ks, auto slot_c) {
@@ -482,7 +490,7 @@ __global__ __launch_bounds__(512, 1) void qmm_gemm_dma8_kernel(QmmArgs a, int nt
         for (int j = 0; j < 4; ++j) acc[i][j] = mfma32<XT>(af[kk][i], bf[kk][j], acc[i][j]);
   };
 
-  const int nk = K / DBK;
+  const int nk = klen / DBK;
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
   using I2 = std::integral_constant<int, 2>;
@@ -527,7 +535,10 @@ __global__ __launch_bounds__(512, 1) void qmm_gemm_dma8_kernel(QmmArgs a, int nt
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int row = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-        if (row < M && col < N) out[static_cast<int64_t>(row) * N + col] = from_f<XT>(acc[i][j][v]);
+        if (row < M && col < N) {
+          if (KSPL == 1) out[static_cast<int64_t>(row) * N + col] = from_f<XT>(acc[i][j][v]);
+          else pt[static_cast<int64_t>(row) * N + col] = acc[i][j][v];
+        }
       }
     }
 }
@@ -971,6 +982,28 @@ hipError_t set_lds_once(size_t bytes) {
   return e;
 }
 
+// Run `launch(part)` into an fp32 workspace of ks partial outputs and sum
+// them into a.out in a fixed order.  The workspace is stream-ordered
+// (hipMallocAsync / hipFreeAsync), so concurrent calls on other streams get
+// their own.
+template <int XT, class F>
+hipError_t splitk_run(const QmmArgs& a, int ks, F&& launch) {
+  const int64_t n = static_cast<int64_t>(a.nbatch) * a.M * a.N;
+  float* part = nullptr;
+  hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&part), static_cast<size_t>(n) * ks * sizeof(float),
+                                a.stream);
+  if (e != hipSuccess) return e;
+  e = launch(part);
+  if (e == hipSuccess) {
+    const int64_t nb = (n + 1023) / 1024;
+    hipLaunchKernelGGL(splitk_reduce_kernel<XT>, dim3(static_cast<unsigned>(nb)), dim3(256), 0, a.stream, part,
+                       static_cast<uint16_t*>(a.out), n, ks);
+    e = hipGetLastError();
+  }
+  const hipError_t f = hipFreeAsync(part, a.stream);
+  return e != hipSuccess ? e : f;
+}
+
 template <int XT, int MODE, int BITS, int TM, int TN>
 hipError_t wr_launch_tile(const QmmArgs& a, int ks, float* part) {
   constexpr int WD = 6;
@@ -1003,20 +1036,7 @@ hipError_t wr_launch(const QmmArgs& a, int G) {
   while (small * ks < 256 && ks < 16 && a.K % (span * ks * 2) == 0 && a.K / (ks * 2) >= 512) ks *= 2;
   (void)G;
   if (ks == 1) return wr_launch_tile<XT, MODE, BITS, 128, 128>(a, 1, nullptr);
-  const int64_t n = static_cast<int64_t>(a.nbatch) * a.M * a.N;
-  float* part = nullptr;
-  hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&part), static_cast<size_t>(n) * ks * sizeof(float),
-                                a.stream);
-  if (e != hipSuccess) return e;
-  e = wr_launch_tile<XT, MODE, BITS, 128, 128>(a, ks, part);
-  if (e == hipSuccess) {
-    const int64_t nb = (n + 1023) / 1024;
-    hipLaunchKernelGGL(splitk_reduce_kernel<XT>, dim3(static_cast<unsigned>(nb)), dim3(256), 0, a.stream, part,
-                       static_cast<uint16_t*>(a.out), n, ks);
-    e = hipGetLastError();
-  }
-  const hipError_t f = hipFreeAsync(part, a.stream);
-  return e != hipSuccess ? e : f;
+  return splitk_run<XT>(a, ks, [&](float* part) { return wr_launch_tile<XT, MODE, BITS, 128, 128>(a, ks, part); });
 }
 
 template <int XT, int MODE, int BITS>
@@ -1039,7 +1059,21 @@ hipError_t gemm_launch_t(const QmmArgs& a) {
     constexpr size_t lds = dma_lds_bytes<BITS, MODE>();
     hipError_t e = set_lds_once<kern>(lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(kern, grid, dim3(512), lds, a.stream, a, ntm, ntn);
+    // few 256x256 tiles: split K over workgroups (whole scale pairs / quads
+    // of groups per split, at least 16 K steps each)
+    const int span = (MODE == AFFINE ? 2 : 4) * (MODE == AFFINE ? a.gs : ModeInfo<MODE>::GS);
+    int ks = 1;
+    while (nblk * a.nbatch * ks < 192 && ks < 16 && a.K % (std::max(span, DBK) * ks * 2) == 0 &&
+           a.K / (ks * 2) >= 16 * DBK)
+      ks *= 2;
+    if (ks > 1) {
+      const dim3 g3(grid.x, grid.y, static_cast<unsigned>(ks));
+      return splitk_run<XT>(a, ks, [&](float* part) {
+        hipLaunchKernelGGL(kern, g3, dim3(512), lds, a.stream, a, ntm, ntn, part);
+        return hipGetLastError();
+      });
+    }
+    hipLaunchKernelGGL(kern, grid, dim3(512), lds, a.stream, a, ntm, ntn, nullptr);
   } else if (a.transpose) {
     constexpr auto kern = qmm_gemm_reg_kernel<XT, MODE, BITS, true>;
     hipError_t e = set_lds_once<kern>(REG_LDS_BYTES);
