@@ -50,7 +50,7 @@ bool qmm_mfma_supported(const QmmArgs& a);
 hipError_t launch_qmm_gemm(const QmmArgs& a);   // 256x256 prefill GEMM
 hipError_t launch_qmm_skinny(const QmmArgs& a); // decode widths 2 <= M <= 64
 bool qmm_skinny_supported(const QmmArgs& a);
-// factored affine 4-bit MFMA kernel for decode widths (x rows <= 2 m tiles)
+// factored affine 4-bit MFMA kernel for decode widths (x rows <= 4 m tiles, <= 32)
 hipError_t launch_qmm_skinny_fac(const QmmArgs& a);
 bool qmm_skinny_fac_supported(const QmmArgs& a);
 // sorted-expert grouped gather_qmm: nflat batch elements, E experts

@@ -463,7 +463,8 @@ hipError_t fac_launch_gb(const QmmArgs& a) {
   while (S < 8 && P / (2 * S) >= 2 && nwg * a.nbatch * S < 4096) S *= 2;
   const dim3 grid(static_cast<unsigned>(nwg), static_cast<unsigned>(a.nbatch));
   if (a.M <= RPT) return fac_launch_s<XT, NT, 1, GB>(a, grid, S);
-  return fac_launch_s<XT, NT, 2, GB>(a, grid, S);
+  if (a.M <= 2 * RPT) return fac_launch_s<XT, NT, 2, GB>(a, grid, S);
+  return fac_launch_s<XT, NT, 4, GB>(a, grid, S);
 }
 template <int XT>
 hipError_t fac_launch(const QmmArgs& a) {
@@ -483,7 +484,7 @@ bool qmm_skinny_fac_supported(const QmmArgs& a) {
   // with fewer than 2048 waves (8 per 32-row tile pair) the split-K skinny
   // kernel keeps more loads in flight
   const int64_t waves = (a.N + 31) / 32 * 8 * a.nbatch;
-  return a.M >= 1 && a.M <= 2 * rpt && waves >= 2048;
+  return a.M >= 1 && a.M <= 4 * rpt && a.M <= 32 && waves >= 2048;
 }
 
 hipError_t launch_qmm_skinny_fac(const QmmArgs& a) {

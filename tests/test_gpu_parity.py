@@ -361,6 +361,32 @@ def test_gather_qmm_sorted_with_lhs_and_invalid(ops):
         assert rel_err(g[i], ref) <= TOL["bf16"]
 
 
+@pytest.mark.parametrize("xdt", ["bf16", "f16"])
+@pytest.mark.parametrize("M", [1, 2])
+def test_gather_qmm_sorted_few_rows(ops, M, xdt):
+    """Sorted grouped gather at K = 2048 with few rows per expert: ragged
+    segments (1..4 batch elements of M x rows), unused experts, an
+    out-of-range expert (NaN rows) and an out-of-range lhs x index (NaN row)."""
+    rng = np.random.default_rng(31 + M)
+    E, N, K = 6, 130, 2048
+    w, s, b = rand_affine(rng, N, K, 64, 4, xdt, lead=(E,))
+    x = oracle.from_float(rng.standard_normal((7, M, K)).astype(np.float32), xdt)
+    rhs = np.array([0, 0, 0, 2, 2, 3, 5, 5, 5, 5, 6], np.int32)      # 6 is out of range; 1, 4 unused
+    lhs = np.array([1, 3, 6, 0, 9, 2, 4, 5, 6, 1, 2], np.int32)      # 9: x index out of range
+    got = ops.gather_qmm(from_np(x, xdt), words_to_torch(w), from_np(s, xdt),
+                         from_np(b, xdt), torch.from_numpy(lhs).cuda(),
+                         torch.from_numpy(rhs).cuda(), sorted_indices=True)
+    g = as_f64(to_np(got, xdt), xdt)
+    assert g.shape == (11, M, N)
+    for i in range(11):
+        if rhs[i] >= E or lhs[i] >= 7:
+            assert np.all(np.isnan(g[i]))
+            continue
+        ref = oracle.qmm(x[lhs[i]], xdt, w[rhs[i]], s[rhs[i]], b[rhs[i]], xdt, True, 64, 4,
+                         odt="f32")
+        assert rel_err(g[i], ref) <= TOL[xdt]
+
+
 @pytest.mark.parametrize("mode", ["affine", "nvfp4"])
 def test_gather_qmm_sorted_many_rows_per_expert(ops, mode):
     """More than 32 rows on one expert exercises the m-tile loop."""
