@@ -13,6 +13,13 @@
  *                                                    in mlx/src/nn/moe.rs:84-170)
  *   iqmm_quantize          <- mlx_quantize          (not bound by ironmlx; makes
  *                                                    the packed inputs)
+ *   iqmm_quantized_swiglu  <- gate/up quantized_matmul + silu * up
+ *                             (mlx/src/nn/mlp.rs:27-33)
+ *   iqmm_gather_qmm_swiglu <- the same per expert (mlx/src/nn/moe.rs:10-33)
+ *   iqmm_dequantize_rows   <- dequantize + take_axis (mlx/src/nn/embedding.rs:62-72)
+ *   iqmm_moe_route / _sort / _combine
+ *                          <- the router, token lists and weighted sum of
+ *                             mlx/src/nn/moe.rs:67-168
  *   iqmm_last_error        <- the thread-local message mlx's error handler
  *                             stores (mlx/src/error.rs:17-55)
  *
@@ -137,6 +144,92 @@ int iqmm_gather_qmm(iqmm_array* res, iqmm_array x, iqmm_array w, iqmm_array scal
 int iqmm_quantize(iqmm_array* res_w, iqmm_array* res_scales, iqmm_array* res_biases,
                   iqmm_array w, iqmm_optional_int group_size, iqmm_optional_int bits,
                   const char* mode, iqmm_stream stream);
+
+/*
+ * Fused SwiGLU over a gate_up weight: w [..., 2I, K*bits/32] holds the gate
+ * rows [0, I) then the up rows [I, 2I) (the fused `gate_up_proj` layout of
+ * mlx/src/model/qwen35.rs:653-658; a Llama gate_proj / up_proj pair stacked
+ * along rows).  out [..., M, I] = silu(x @ gate^T) * (x @ up^T), rounded as
+ * the unfused composition of mlx/src/nn/mlp.rs:27-33 rounds it (gate and up
+ * stored in x's dtype, then sigmoid, the silu product and the up product each
+ * rounded).  Replaces the gate / up quantized_matmul pair plus silu and
+ * multiply in MLP::forward_with_stream (mlx/src/nn/mlp.rs:27-33).  transpose
+ * is implied (true); other arguments as iqmm_quantized_matmul.
+ */
+int iqmm_quantized_swiglu(iqmm_array* res, iqmm_array x, iqmm_array w, iqmm_array scales,
+                          iqmm_array biases, iqmm_optional_int group_size, iqmm_optional_int bits,
+                          const char* mode, iqmm_stream stream);
+
+/*
+ * gather_qmm over stacked gate_up experts w [E, 2I, K*bits/32] followed by
+ * the SwiGLU of iqmm_quantized_swiglu: out [..., M, I].  Replaces the gate /
+ * up products and silu * up of each Expert (mlx/src/nn/moe.rs:10-33) inside
+ * the per-expert loop of mlx/src/nn/moe.rs:117-143.  Index arguments as
+ * iqmm_gather_qmm.
+ */
+int iqmm_gather_qmm_swiglu(iqmm_array* res, iqmm_array x, iqmm_array w, iqmm_array scales,
+                           iqmm_array biases, iqmm_array lhs_indices, iqmm_array rhs_indices,
+                           iqmm_optional_int group_size, iqmm_optional_int bits, const char* mode,
+                           bool sorted_indices, iqmm_stream stream);
+
+/*
+ * Row gather of a quantized table: out[i, :] = dequantize(w)[indices[i], :]
+ * without dequantizing the table.  Replaces dequantize + take_axis in
+ * QuantizedEmbedding::forward (mlx/src/nn/embedding.rs:62-72).
+ *   w [rows, K*bits/32], scales / biases [rows, K/gs] as iqmm_dequantize
+ *   indices: integer array of any shape; negative values count from the end
+ *   out indices.shape + [K], dtype as iqmm_dequantize (bit-identical rows)
+ * Indices outside [-rows, rows) give NaN rows.
+ */
+int iqmm_dequantize_rows(iqmm_array* res, iqmm_array w, iqmm_array scales, iqmm_array biases,
+                         iqmm_array indices, iqmm_optional_int group_size, iqmm_optional_int bits,
+                         const char* mode, iqmm_optional_dtype dtype, iqmm_stream stream);
+
+/*
+ * MoE router on the device: softmax over the experts of each token, top-k,
+ * optional normalisation.  Replaces mlx/src/nn/moe.rs:67-82 and the host
+ * read-back of :86-90.
+ *   logits       [T, E] float32 | float16 | bfloat16
+ *   res_scores   [T, k] float32: the selected probabilities (stored in the
+ *                logits' dtype, as MLX's softmax output is) or, with
+ *                norm_topk_prob, p / sum(p of the k) rounded to that dtype
+ *   res_experts  [T, k] int32: experts by descending probability, ties to the
+ *                lower index (a stable argsort of -p, as moe.rs:72-73)
+ * 1 <= k <= min(E, 32), E <= 2048.
+ */
+int iqmm_moe_route(iqmm_array* res_scores, iqmm_array* res_experts, iqmm_array logits, int k,
+                   bool norm_topk_prob, iqmm_stream stream);
+
+/*
+ * Stable sort of the (token, slot) rows of a routing by expert, producing the
+ * sorted_indices form of iqmm_gather_qmm.  Replaces the per-expert token lists
+ * of mlx/src/nn/moe.rs:92-104.
+ *   experts          [T, k] int32 (n = T*k rows, row r = t*k + slot)
+ *   res_tokens       [n] int32: token of each sorted row (gather_qmm lhs_indices)
+ *   res_sorted       [n] int32: expert of each sorted row (rhs_indices);
+ *                    ids outside [0, num_experts) sort last
+ *   res_inverse      [n] int32: sorted position of row r
+ *   res_offsets      [num_experts + 1] int32: first sorted row of each expert,
+ *                    offsets[num_experts] = number of valid rows (may be a
+ *                    NULL pointer to skip)
+ * n <= 32768.
+ */
+int iqmm_moe_sort(iqmm_array* res_tokens, iqmm_array* res_sorted, iqmm_array* res_inverse,
+                  iqmm_array* res_offsets, iqmm_array experts, int num_experts, iqmm_stream stream);
+
+/*
+ * Weighted combine of expert outputs: out[t, :] = sum over the k slots of t,
+ * in ascending expert order, of float32(y[inverse[t*k + slot], :]) * score,
+ * accumulated sequentially in float32 as mlx/src/nn/moe.rs:146-168 does.
+ *   y        [n, D] (or [n, 1, D]) float32 | float16 | bfloat16, sorted rows
+ *   inverse  [T, k] or [n] int32 from iqmm_moe_sort
+ *   experts  [T, k] int32, scores [T, k] float32 from iqmm_moe_route
+ *   res      [T, D] float32
+ * Slots whose expert is outside [0, num_experts) are skipped, as the
+ * reference skips them (moe.rs:99); a token with none gets a zero row.
+ */
+int iqmm_moe_combine(iqmm_array* res, iqmm_array y, iqmm_array inverse, iqmm_array experts,
+                     iqmm_array scores, int num_experts, iqmm_stream stream);
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* iqmm_last_error(void);

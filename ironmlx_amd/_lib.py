@@ -31,6 +31,8 @@ class OptionalDtype(ctypes.Structure):
 
 
 EXPORTS = ("iqmm_quantized_matmul", "iqmm_dequantize", "iqmm_gather_qmm", "iqmm_quantize",
+           "iqmm_quantized_swiglu", "iqmm_gather_qmm_swiglu", "iqmm_dequantize_rows",
+           "iqmm_moe_route", "iqmm_moe_sort", "iqmm_moe_combine",
            "iqmm_last_error", "iqmm_version")
 
 _lib = None
@@ -60,6 +62,19 @@ def load() -> ctypes.CDLL:
     L.iqmm_gather_qmm.restype = ctypes.c_int
     L.iqmm_quantize.argtypes = [P, P, P, A, OI, OI, cs, vp]
     L.iqmm_quantize.restype = ctypes.c_int
+    L.iqmm_quantized_swiglu.argtypes = [P, A, A, A, A, OI, OI, cs, vp]
+    L.iqmm_quantized_swiglu.restype = ctypes.c_int
+    L.iqmm_gather_qmm_swiglu.argtypes = [P, A, A, A, A, A, A, OI, OI, cs, b, vp]
+    L.iqmm_gather_qmm_swiglu.restype = ctypes.c_int
+    L.iqmm_dequantize_rows.argtypes = [P, A, A, A, A, OI, OI, cs, OD, vp]
+    L.iqmm_dequantize_rows.restype = ctypes.c_int
+    i = ctypes.c_int
+    L.iqmm_moe_route.argtypes = [P, P, A, i, b, vp]
+    L.iqmm_moe_route.restype = ctypes.c_int
+    L.iqmm_moe_sort.argtypes = [P, P, P, P, A, i, vp]
+    L.iqmm_moe_sort.restype = ctypes.c_int
+    L.iqmm_moe_combine.argtypes = [P, A, A, A, A, i, vp]
+    L.iqmm_moe_combine.restype = ctypes.c_int
     L.iqmm_last_error.restype = ctypes.c_char_p
     L.iqmm_last_error.argtypes = []
     L.iqmm_version.restype = ctypes.c_char_p

@@ -205,6 +205,33 @@ hipError_t run_qmm(QmmArgs& a) {
   return a.transpose ? launch_qmv(a) : launch_qvm(a);
 }
 
+int elt_size(int dt) { return dt == IQMM_FLOAT32 ? 4 : 2; }
+
+// Fused SwiGLU over a gate_up weight of 2I rows (a.N = I outputs): the M = 1
+// GEMV reduces each gate row and its up row in one wave and applies the
+// SwiGLU in its epilogue; every other shape computes the [.., M, 2I] product
+// into a stream-ordered workspace with the regular kernels (`product`) and
+// then runs the elementwise SwiGLU over it.
+template <class F>
+hipError_t run_glu(QmmArgs& a, bool try_fused, F&& product) {
+  a.glu = 1;
+  if (try_fused && qmv_q4_m1_supported(a)) return launch_qmv_q4_m1(a);
+  a.glu = 0;
+  const int64_t I = a.N, rows = a.nbatch * a.M;
+  void* out = a.out;
+  void* ws = nullptr;
+  hipError_t e = hipMallocAsync(&ws, static_cast<size_t>(rows) * 2 * I * elt_size(a.xdt), a.stream);
+  if (e != hipSuccess) return e;
+  a.N = static_cast<int>(2 * I);
+  a.out = ws;
+  e = product(a);
+  if (e == hipSuccess) e = launch_swiglu_rows(ws, out, rows, I, a.xdt, a.stream);
+  const hipError_t f = hipFreeAsync(ws, a.stream);
+  a.N = static_cast<int>(I);
+  a.out = out;
+  return e != hipSuccess ? e : f;
+}
+
 // common core of quantized_matmul / gather_qmm once batch mapping is known
 int qmm_common(const char* op, iqmm_array* res, const iqmm_array& x, const iqmm_array& w,
                const iqmm_array& s, const iqmm_array& b, bool transpose, const QParams& q,
@@ -254,16 +281,27 @@ const char* iqmm_last_error(void) { return g_last_error.c_str(); }
 
 const char* iqmm_version(void) { return "iqmm 0.1 gfx950"; }
 
-int iqmm_quantized_matmul(iqmm_array* res, iqmm_array x, iqmm_array w, iqmm_array scales,
-                          iqmm_array biases, bool transpose, iqmm_optional_int group_size,
-                          iqmm_optional_int bits, const char* mode, iqmm_stream stream) {
-  const char* op = "quantized_matmul";
+}  // extern "C"
+
+namespace iqmm {
+namespace {
+// quantized_matmul, and with glu its fused SwiGLU form (N = 2I weight rows -> I outputs)
+int qmm_entry(const char* op, iqmm_array* res, iqmm_array x, iqmm_array w, iqmm_array scales,
+              iqmm_array biases, bool transpose, iqmm_optional_int group_size,
+              iqmm_optional_int bits, const char* mode, iqmm_stream stream, bool glu) {
   g_last_error.clear();
   QParams q;
   if (resolve(op, mode, group_size, bits, q)) return 1;
   int64_t M, N, K;
   int sdt;
   if (qmm_common(op, res, x, w, scales, biases, transpose, q, M, N, K, &sdt)) return 1;
+  const int64_t Nw = N;  // weight rows
+  if (glu) {
+    if (N % 2 != 0)
+      return fail("[%s] the fused gate_up weight must have an even number of rows (gate then up), got %lld.", op,
+                  (long long)N);
+    N /= 2;
+  }
 
   QmmArgs a{};
   const int xb_nd = x.ndim >= 2 ? x.ndim - 2 : 0, wb_nd = w.ndim - 2;
@@ -309,15 +347,37 @@ int iqmm_quantized_matmul(iqmm_array* res, iqmm_array x, iqmm_array w, iqmm_arra
   for (int i = 0; i < wb_nd; ++i) nwm *= w.shape[i];
   a.bm.nx = nxm; a.bm.nw = nwm; a.bm.lhs = nullptr; a.bm.rhs = nullptr;
   a.stream = st;
-  hipError_t e = run_qmm(a);
+  (void)Nw;
+  hipError_t e = glu ? run_glu(a, true, [](QmmArgs& p) { return run_qmm(p); }) : run_qmm(a);
   return e == hipSuccess ? 0 : hip_fail(op, e);
 }
+}  // namespace
+}  // namespace iqmm
 
-int iqmm_gather_qmm(iqmm_array* res, iqmm_array x, iqmm_array w, iqmm_array scales,
-                    iqmm_array biases, iqmm_array lhs, iqmm_array rhs, bool transpose,
-                    iqmm_optional_int group_size, iqmm_optional_int bits, const char* mode,
-                    bool sorted_indices, iqmm_stream stream) {
-  const char* op = "gather_qmm";
+extern "C" {
+
+int iqmm_quantized_matmul(iqmm_array* res, iqmm_array x, iqmm_array w, iqmm_array scales,
+                          iqmm_array biases, bool transpose, iqmm_optional_int group_size,
+                          iqmm_optional_int bits, const char* mode, iqmm_stream stream) {
+  return qmm_entry("quantized_matmul", res, x, w, scales, biases, transpose, group_size, bits, mode, stream,
+                   false);
+}
+
+int iqmm_quantized_swiglu(iqmm_array* res, iqmm_array x, iqmm_array w, iqmm_array scales,
+                          iqmm_array biases, iqmm_optional_int group_size, iqmm_optional_int bits,
+                          const char* mode, iqmm_stream stream) {
+  return qmm_entry("quantized_swiglu", res, x, w, scales, biases, true, group_size, bits, mode, stream, true);
+}
+
+}  // extern "C"
+
+namespace iqmm {
+namespace {
+// gather_qmm, and with glu its fused SwiGLU form over stacked gate_up experts
+int gather_entry(const char* op, iqmm_array* res, iqmm_array x, iqmm_array w, iqmm_array scales,
+                 iqmm_array biases, iqmm_array lhs, iqmm_array rhs, bool transpose,
+                 iqmm_optional_int group_size, iqmm_optional_int bits, const char* mode,
+                 bool sorted_indices, iqmm_stream stream, bool glu) {
   g_last_error.clear();
   QParams q;
   if (resolve(op, mode, group_size, bits, q)) return 1;
@@ -325,6 +385,12 @@ int iqmm_gather_qmm(iqmm_array* res, iqmm_array x, iqmm_array w, iqmm_array scal
   int64_t M, N, K;
   int sdt;
   if (qmm_common(op, res, x, w, scales, biases, transpose, q, M, N, K, &sdt)) return 1;
+  if (glu) {
+    if (N % 2 != 0)
+      return fail("[%s] the fused gate_up weight must have an even number of rows (gate then up), got %lld.", op,
+                  (long long)N);
+    N /= 2;
+  }
   const int xb_nd = x.ndim - 2, wb_nd = w.ndim - 2;
   QmmArgs a{};
   // index arrays: absent -> arange over the operand's batch, shaped like it
@@ -370,18 +436,46 @@ int iqmm_gather_qmm(iqmm_array* res, iqmm_array x, iqmm_array w, iqmm_array scal
   // output batch one-to-one, so expert segments are contiguous in it
   const bool one_to_one = present(rhs) && numel(rhs) == a.nbatch &&
                           (present(lhs) ? numel(lhs) == a.nbatch : nxm == a.nbatch);
-  if (sorted_indices && one_to_one && gather_sorted_supported(a) && nwm + 1 <= 65535) {
-    hipError_t e = launch_gather_sorted(a, a.nbatch, nwm);
-    return e == hipSuccess ? 0 : hip_fail(op, e);
-  }
-  hipError_t e = run_qmm(a);
+  const bool grouped = sorted_indices && one_to_one && nwm + 1 <= 65535;
+  auto product = [&](QmmArgs& p) {
+    if (grouped && gather_sorted_supported(p)) return launch_gather_sorted(p, p.nbatch, nwm);
+    return run_qmm(p);
+  };
+  // few rows: the fused GEMV (one wave per output pair); many sorted rows:
+  // the grouped kernel, whose weight tiles serve every row of an expert
+  constexpr int64_t kFusedRows = 16;
+  hipError_t e = glu ? run_glu(a, !grouped || a.nbatch * a.M <= kFusedRows, product) : product(a);
   return e == hipSuccess ? 0 : hip_fail(op, e);
 }
+}  // namespace
+}  // namespace iqmm
 
-int iqmm_dequantize(iqmm_array* res, iqmm_array w, iqmm_array scales, iqmm_array biases,
+extern "C" {
+
+int iqmm_gather_qmm(iqmm_array* res, iqmm_array x, iqmm_array w, iqmm_array scales,
+                    iqmm_array biases, iqmm_array lhs, iqmm_array rhs, bool transpose,
                     iqmm_optional_int group_size, iqmm_optional_int bits, const char* mode,
-                    iqmm_optional_dtype dtype, iqmm_stream stream) {
-  const char* op = "dequantize";
+                    bool sorted_indices, iqmm_stream stream) {
+  return gather_entry("gather_qmm", res, x, w, scales, biases, lhs, rhs, transpose, group_size, bits, mode,
+                      sorted_indices, stream, false);
+}
+
+int iqmm_gather_qmm_swiglu(iqmm_array* res, iqmm_array x, iqmm_array w, iqmm_array scales,
+                           iqmm_array biases, iqmm_array lhs, iqmm_array rhs,
+                           iqmm_optional_int group_size, iqmm_optional_int bits, const char* mode,
+                           bool sorted_indices, iqmm_stream stream) {
+  return gather_entry("gather_qmm_swiglu", res, x, w, scales, biases, lhs, rhs, true, group_size, bits, mode,
+                      sorted_indices, stream, true);
+}
+
+}  // extern "C"
+
+namespace iqmm {
+namespace {
+// dequantize, and with an index array the row gather of an embedding table
+int deq_entry(const char* op, iqmm_array* res, iqmm_array w, iqmm_array scales, iqmm_array biases,
+              const iqmm_array* idx, iqmm_optional_int group_size, iqmm_optional_int bits,
+              const char* mode, iqmm_optional_dtype dtype, iqmm_stream stream) {
   g_last_error.clear();
   QParams q;
   if (resolve(op, mode, group_size, bits, q)) return 1;
@@ -400,18 +494,48 @@ int iqmm_dequantize(iqmm_array* res, iqmm_array w, iqmm_array scales, iqmm_array
   }
   std::vector<int64_t> out_shape(w.shape, w.shape + w.ndim);
   out_shape.back() = K;
+  if (idx) {
+    if (w.ndim != 2) return fail("[%s] the quantized table must be 2D [rows, K*bits/32], got %s.", op, shape_str(w).c_str());
+    if (!present(*idx) || !is_index(idx->dtype))
+      return fail("[%s] indices must be an integer array, got %s.", op, present(*idx) ? dt_name(idx->dtype) : "none");
+    out_shape.assign(idx->shape, idx->shape + idx->ndim);
+    out_shape.push_back(K);
+  }
   bool query;
   if (set_or_check_res(op, res, out_shape, odt, &query)) return 1;
   if (query) return 0;
   ConvArgs a{};
   a.w = static_cast<const uint32_t*>(w.data); a.s = scales.data; a.b = biases.data; a.out = res->data;
   a.rows = numel(w) / (wlast > 0 ? wlast : 1);
+  if (idx) {
+    a.table_rows = a.rows;
+    a.rows = numel(*idx);
+    a.idx = idx->data;
+    a.idx_dt = idx->dtype;
+    if (a.rows == 0) return 0;
+  }
   if (wlast == 0) return 0;
   if (K > 0x7fffffffLL) return fail("[%s] row too long.", op);
   a.K = static_cast<int>(K); a.gs = q.gs; a.bits = q.bits; a.mode = q.mode; a.sdt = sdt; a.odt = odt;
   a.stream = static_cast<hipStream_t>(stream);
   hipError_t e = launch_dequantize(a);
   return e == hipSuccess ? 0 : hip_fail(op, e);
+}
+}  // namespace
+}  // namespace iqmm
+
+extern "C" {
+
+int iqmm_dequantize(iqmm_array* res, iqmm_array w, iqmm_array scales, iqmm_array biases,
+                    iqmm_optional_int group_size, iqmm_optional_int bits, const char* mode,
+                    iqmm_optional_dtype dtype, iqmm_stream stream) {
+  return deq_entry("dequantize", res, w, scales, biases, nullptr, group_size, bits, mode, dtype, stream);
+}
+
+int iqmm_dequantize_rows(iqmm_array* res, iqmm_array w, iqmm_array scales, iqmm_array biases,
+                         iqmm_array indices, iqmm_optional_int group_size, iqmm_optional_int bits,
+                         const char* mode, iqmm_optional_dtype dtype, iqmm_stream stream) {
+  return deq_entry("dequantize_rows", res, w, scales, biases, &indices, group_size, bits, mode, dtype, stream);
 }
 
 int iqmm_quantize(iqmm_array* res_w, iqmm_array* res_scales, iqmm_array* res_biases,
@@ -453,6 +577,93 @@ int iqmm_quantize(iqmm_array* res_w, iqmm_array* res_scales, iqmm_array* res_bia
   a.K = static_cast<int>(K); a.gs = q.gs; a.bits = q.bits; a.mode = q.mode; a.sdt = w.dtype;
   a.stream = static_cast<hipStream_t>(stream);
   hipError_t e = launch_quantize(a);
+  return e == hipSuccess ? 0 : hip_fail(op, e);
+}
+
+
+int iqmm_moe_route(iqmm_array* res_scores, iqmm_array* res_experts, iqmm_array logits, int k,
+                   bool norm_topk_prob, iqmm_stream stream) {
+  const char* op = "moe_route";
+  g_last_error.clear();
+  if (!present(logits) || logits.ndim != 2) return fail("[%s] logits must be 2D [tokens, experts], got %s.", op, shape_str(logits).c_str());
+  if (!is_float(logits.dtype)) return fail("[%s] logits must be floating point, got %s.", op, dt_name(logits.dtype));
+  const int64_t T = logits.shape[0], E = logits.shape[1];
+  if (E < 1 || E > 2048) return fail("[%s] the number of experts must be in [1, 2048], got %lld.", op, (long long)E);
+  if (k < 1 || k > 32 || k > E) return fail("[%s] k must be in [1, min(experts, 32)], got %d.", op, k);
+  if (T > 0x7fffffffLL / 4) return fail("[%s] too many tokens.", op);
+  const std::vector<int64_t> shp = {T, k};
+  bool q1, q2;
+  if (set_or_check_res(op, res_scores, shp, IQMM_FLOAT32, &q1)) return 1;
+  if (set_or_check_res(op, res_experts, shp, IQMM_INT32, &q2)) return 1;
+  if (q1 || q2) {
+    if (!(q1 && q2)) return fail("[%s] either all result buffers are allocated or none.", op);
+    return 0;
+  }
+  hipError_t e = launch_moe_route(logits.data, logits.dtype, static_cast<float*>(res_scores->data),
+                                  static_cast<int32_t*>(res_experts->data), static_cast<int>(T), static_cast<int>(E), k,
+                                  norm_topk_prob, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? 0 : hip_fail(op, e);
+}
+
+int iqmm_moe_sort(iqmm_array* res_tokens, iqmm_array* res_sorted, iqmm_array* res_inverse,
+                  iqmm_array* res_offsets, iqmm_array experts, int num_experts, iqmm_stream stream) {
+  const char* op = "moe_sort";
+  g_last_error.clear();
+  if (!present(experts) || experts.ndim != 2 || experts.dtype != IQMM_INT32)
+    return fail("[%s] experts must be a 2D int32 array [tokens, k], got %s %s.", op, shape_str(experts).c_str(),
+                dt_name(experts.dtype));
+  if (num_experts < 1 || num_experts > 65535) return fail("[%s] num_experts must be in [1, 65535], got %d.", op, num_experts);
+  const int64_t n = numel(experts), k = experts.shape[1];
+  if (n > 32768) return fail("[%s] at most 32768 (token, slot) rows are sorted in one call, got %lld.", op, (long long)n);
+  const std::vector<int64_t> shp = {n}, oshp = {static_cast<int64_t>(num_experts) + 1};
+  bool q1, q2, q3, q4 = false;
+  if (set_or_check_res(op, res_tokens, shp, IQMM_INT32, &q1)) return 1;
+  if (set_or_check_res(op, res_sorted, shp, IQMM_INT32, &q2)) return 1;
+  if (set_or_check_res(op, res_inverse, shp, IQMM_INT32, &q3)) return 1;
+  if (res_offsets && set_or_check_res(op, res_offsets, oshp, IQMM_INT32, &q4)) return 1;
+  if (q1 || q2 || q3 || q4) {
+    if (!(q1 && q2 && q3 && (!res_offsets || q4))) return fail("[%s] either all result buffers are allocated or none.", op);
+    return 0;
+  }
+  if (n == 0) {
+    if (!res_offsets) return 0;
+    // int32 zeros have the bits of float32 zeros; a fill kernel (not a
+    // memset node) keeps the call capturable in a HIP graph
+    hipError_t e = fill_zero(res_offsets->data, IQMM_FLOAT32, static_cast<int64_t>(num_experts) + 1,
+                             static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? 0 : hip_fail(op, e);
+  }
+  hipError_t e = launch_moe_sort(static_cast<const int32_t*>(experts.data), static_cast<int>(n), static_cast<int>(k),
+                                 num_experts, static_cast<int32_t*>(res_tokens->data),
+                                 static_cast<int32_t*>(res_sorted->data), static_cast<int32_t*>(res_inverse->data),
+                                 res_offsets ? static_cast<int32_t*>(res_offsets->data) : nullptr,
+                                 static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? 0 : hip_fail(op, e);
+}
+
+int iqmm_moe_combine(iqmm_array* res, iqmm_array y, iqmm_array inverse, iqmm_array experts,
+                     iqmm_array scores, int num_experts, iqmm_stream stream) {
+  const char* op = "moe_combine";
+  g_last_error.clear();
+  if (!present(experts) || experts.ndim != 2 || experts.dtype != IQMM_INT32)
+    return fail("[%s] experts must be a 2D int32 array [tokens, k].", op);
+  const int64_t T = experts.shape[0], k = experts.shape[1];
+  if (!present(scores) || scores.dtype != IQMM_FLOAT32 || numel(scores) != T * k)
+    return fail("[%s] scores must be float32 with the experts' %lld entries.", op, (long long)(T * k));
+  if (!present(inverse) || inverse.dtype != IQMM_INT32 || numel(inverse) != T * k)
+    return fail("[%s] inverse must be int32 with the experts' %lld entries.", op, (long long)(T * k));
+  if (!present(y) || y.ndim < 2 || !is_float(y.dtype)) return fail("[%s] y must be a floating array [rows, D].", op);
+  const int64_t D = y.shape[y.ndim - 1];
+  const int64_t n = D > 0 ? numel(y) / D : 0;
+  if (T > 0x7fffffffLL) return fail("[%s] too many tokens.", op);
+  const std::vector<int64_t> shp = {T, D};
+  bool q;
+  if (set_or_check_res(op, res, shp, IQMM_FLOAT32, &q)) return 1;
+  if (q) return 0;
+  hipError_t e = launch_moe_combine(y.data, y.dtype, static_cast<const int32_t*>(inverse.data),
+                                    static_cast<const int32_t*>(experts.data), static_cast<const float*>(scores.data),
+                                    static_cast<float*>(res->data), static_cast<int>(T), static_cast<int>(k), D,
+                                    num_experts, n, static_cast<hipStream_t>(stream));
   return e == hipSuccess ? 0 : hip_fail(op, e);
 }
 

@@ -62,6 +62,42 @@ __device__ __forceinline__ typename Store<DT>::T from_f(float v) {
   else return f_to_bf16(v);
 }
 
+// exp(x): Cody-Waite reduction x = n ln2 + r (|r| <= ln2 / 2; ln2 split into
+// a 16-bit head, so n * head is exact, and a tail), the degree-7 Taylor
+// polynomial of e^r in Horner form with explicit fma, then a 2^n scale.  Each
+// step is a correctly rounded IEEE operation, so results are reproducible
+// bit for bit on the host (within 2 ulp of exp).
+__device__ __forceinline__ float iq_expf(float x) {
+  if (x != x) return x;
+  if (x > 88.7228394f) return __builtin_inff();
+  if (x < -103.972084f) return 0.0f;
+  const float n = __builtin_rintf(x * 1.44269502f);
+  float r = __builtin_fmaf(-n, 0.693145751953125f, x);
+  r = __builtin_fmaf(-n, 1.42860682e-6f, r);
+  float p = 1.0f / 5040.0f;
+  p = __builtin_fmaf(p, r, 1.0f / 720.0f);
+  p = __builtin_fmaf(p, r, 1.0f / 120.0f);
+  p = __builtin_fmaf(p, r, 1.0f / 24.0f);
+  p = __builtin_fmaf(p, r, 1.0f / 6.0f);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  return __builtin_ldexpf(p, static_cast<int>(n));
+}
+
+// SwiGLU of one (gate, up) pair of fp32 sums, rounded the way the unfused
+// composition rounds it: gate and up are first stored in the output type
+// (they are quantized_matmul outputs), then silu(g) = g * sigmoid(g) and the
+// product with up are separate elementwise ops, each rounded to the output
+// type (mlx/src/nn/activations.rs:7-10, mlx/src/nn/mlp.rs:27-33).
+template <int DT>
+__device__ __forceinline__ typename Store<DT>::T swiglu_out(float g, float u) {
+  const float gr = to_f<DT>(from_f<DT>(g)), ur = to_f<DT>(from_f<DT>(u));
+  const float sg = to_f<DT>(from_f<DT>(1.0f / (1.0f + iq_expf(-gr))));
+  const float a = to_f<DT>(from_f<DT>(gr * sg));
+  return from_f<DT>(a * ur);
+}
+
 // -------------------------------------------------------------- fp element codes
 // e2m1 code (4 bits, sign in bit 3) -> value / 2^14 as fp16 bits
 __device__ __forceinline__ float e2m1_to_f(uint32_t c) {

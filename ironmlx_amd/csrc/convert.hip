@@ -1,9 +1,13 @@
 // convert.hip — dequantize and quantize on the GPU.
 //
 // dequantize (mlx/src/ops.rs:653-686; caller mlx/src/nn/embedding.rs:62-72):
-//   one thread per 32-code chunk: `bits` words in, 32 values out, bit-exact:
+//   one thread per 32-code chunk: `bits` words in, 32 values out, bit-exact;
+//   with an index array, output row i is table row idx[i] (the embedding
+//   lookup without dequantizing the whole table):
 //   affine  v = rn(rn(s * q) + b)  (multiply and add rounded separately),
 //   fp      v = rn(elem(q) * scale), then RNE to the output dtype.
+// swiglu rows: the elementwise SwiGLU step of a fused gate_up product
+//   (mlx/src/nn/mlp.rs:27-33), rounded like the unfused composition.
 // quantize (mlx_quantize; makes the packed inputs):
 //   one thread per quantization group, same arithmetic as MLX's per-group
 //   rule (see oracle/iqmm_oracle.c for the restated rule), so codes, scales
@@ -23,10 +27,21 @@ __global__ __launch_bounds__(256) void dequant_kernel(ConvArgs a, int64_t nchunk
   constexpr bool AFF = MODE == AFFINE;
   const int K = a.K;
   const int cpr = (K + 31) >> 5;                 // chunks per row
-  const int64_t row = id / cpr;
-  const int c = static_cast<int>(id - row * cpr);
+  const int64_t orow = id / cpr;                 // output row
+  const int c = static_cast<int>(id - orow * cpr);
   const int k0 = c * 32;
   const int ncode = min(32, K - k0);
+  OS* dst = static_cast<OS*>(a.out) + orow * K + k0;
+  // row gather: output row i takes table row idx[i] (negative from the end)
+  int64_t row = orow;
+  if (a.idx != nullptr) {
+    row = load_index(a.idx, a.idx_dt, orow);
+    if (row < 0) row += a.table_rows;
+    if (row < 0 || row >= a.table_rows) {
+      for (int j = 0; j < ncode; ++j) dst[j] = from_f<ODT>(__builtin_nanf(""));
+      return;
+    }
+  }
   const int64_t wpr = static_cast<int64_t>(K) * BITS / 32;
   const uint32_t* src = a.w + row * wpr + static_cast<int64_t>(c) * BITS;
   uint32_t wd[BITS];
@@ -57,7 +72,6 @@ __global__ __launch_bounds__(256) void dequant_kernel(ConvArgs a, int64_t nchunk
     }
     vals[j] = from_f<ODT>(v);
   }
-  OS* dst = static_cast<OS*>(a.out) + row * K + k0;
   if (ncode == 32 && sizeof(OS) == 2) {
     uint4* d4 = reinterpret_cast<uint4*>(dst);
 #pragma unroll
@@ -251,6 +265,44 @@ hipError_t launch_dequantize(const ConvArgs& a) {
     case BF16: return deq_by_sdt<BF16>(a, nchunks, grid);
   }
   return hipErrorInvalidValue;
+}
+
+// SwiGLU epilogue of a fused gate_up product: gu [rows, 2n] -> out [rows, n]
+template <int DT>
+__global__ __launch_bounds__(256) void swiglu_rows_kernel(const typename Store<DT>::T* gu,
+                                                          typename Store<DT>::T* out, int64_t rows,
+                                                          int64_t n) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= rows * n) return;
+  const int64_t r = i / n, c = i - r * n;
+  const typename Store<DT>::T* src = gu + r * 2 * n;
+  out[i] = swiglu_out<DT>(to_f<DT>(src[c]), to_f<DT>(src[n + c]));
+}
+
+hipError_t launch_swiglu_rows(const void* gu, void* out, int64_t rows, int64_t n, int dt,
+                              hipStream_t st) {
+  const int64_t tot = rows * n;
+  if (tot == 0) return hipSuccess;
+  const int64_t nblk = (tot + 255) / 256;
+  if (nblk > 0x7fffffffLL) return hipErrorInvalidConfiguration;
+  const dim3 grid(static_cast<unsigned>(nblk));
+  switch (dt) {
+    case F32:
+      hipLaunchKernelGGL(swiglu_rows_kernel<F32>, grid, dim3(256), 0, st, static_cast<const float*>(gu),
+                         static_cast<float*>(out), rows, n);
+      break;
+    case F16:
+      hipLaunchKernelGGL(swiglu_rows_kernel<F16>, grid, dim3(256), 0, st, static_cast<const uint16_t*>(gu),
+                         static_cast<uint16_t*>(out), rows, n);
+      break;
+    case BF16:
+      hipLaunchKernelGGL(swiglu_rows_kernel<BF16>, grid, dim3(256), 0, st, static_cast<const uint16_t*>(gu),
+                         static_cast<uint16_t*>(out), rows, n);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
 hipError_t launch_quantize(const ConvArgs& a) {

@@ -24,6 +24,9 @@ struct QmmArgs {
   int64_t nbatch;
   BatchMap bm;
   hipStream_t stream;
+  // fused SwiGLU (qmv_q4 only): w holds 2N rows, gate [0, N) and up [N, 2N);
+  // out[:, n] = silu(x . gate_n) * (x . up_n)
+  int glu;
 };
 
 // Dequantize / quantize problems over `rows` rows of K values.
@@ -36,9 +39,12 @@ struct ConvArgs {
   uint32_t* wq;       // quantize outputs
   void* sq;
   void* bq;
-  int64_t rows;
+  int64_t rows;       // rows produced (dequantize) or quantized
   int K, gs, bits, mode, sdt, odt;
   hipStream_t stream;
+  const void* idx;    // dequantize row gather: table row of each output row, or nullptr
+  int idx_dt;         // I32 / U32 / I64
+  int64_t table_rows; // rows of the packed table (index bound)
 };
 
 hipError_t launch_qmv(const QmmArgs& a);        // transpose=true, small M, VALU
@@ -59,5 +65,16 @@ bool gather_sorted_supported(const QmmArgs& a);
 bool qmm_gemm_supported(const QmmArgs& a);
 hipError_t launch_dequantize(const ConvArgs& a);
 hipError_t launch_quantize(const ConvArgs& a);
+// SwiGLU over a [rows, 2N] product (gate | up halves) -> [rows, N]
+hipError_t launch_swiglu_rows(const void* gu, void* out, int64_t rows, int64_t n, int dt,
+                              hipStream_t st);
+// MoE routing: softmax / top-k, the stable sort by expert, the weighted combine
+hipError_t launch_moe_route(const void* logits, int dt, float* scores, int32_t* experts, int T, int E, int k,
+                            bool norm, hipStream_t st);
+hipError_t launch_moe_sort(const int32_t* experts, int n, int k, int E, int32_t* tokens, int32_t* sorted,
+                           int32_t* inverse, int32_t* offsets, hipStream_t st);
+hipError_t launch_moe_combine(const void* y, int dt, const int32_t* inverse, const int32_t* experts,
+                              const float* scores, float* out, int T, int k, int64_t D, int E, int64_t n,
+                              hipStream_t st);
 
 }  // namespace iqmm

@@ -1,0 +1,258 @@
+// moe.hip — the MoE routing around gather_qmm, on the device.
+//
+// route   (mlx/src/nn/moe.rs:67-82): per token, softmax over the experts in
+//         fp32 with the probabilities stored in the logits' dtype, the k
+//         largest by a stable descending order (ties to the lower expert id,
+//         as a stable argsort of -p), and optionally p / sum(p of the k), each
+//         result rounded to the logits' dtype.  One wave per token.
+// sort    (mlx/src/nn/moe.rs:92-104): the (token, slot) rows ordered by
+//         expert, rows of one expert kept in (token, slot) order.  One
+//         workgroup bitonic-sorts unique 32-bit keys expert * n + row in LDS.
+// combine (mlx/src/nn/moe.rs:146-168): per token, the expert rows times
+//         their scores summed in fp32 in ascending expert order, the first
+//         product taken as is and each further one added, as the reference's
+//         row_sum chain does.
+#include <atomic>
+
+#include "launch.h"
+
+namespace iqmm {
+
+#pragma clang fp contract(off)
+
+namespace {
+
+__device__ __forceinline__ float wave_max(float v) {
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// PL = probabilities per lane (E <= 64 * PL)
+template <int DT, int PL>
+__global__ __launch_bounds__(256) void moe_route_kernel(const typename Store<DT>::T* logits, float* scores,
+                                                        int32_t* experts, int T, int E, int k, int norm) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;  // wave-uniform
+  const typename Store<DT>::T* row = logits + static_cast<int64_t>(t) * E;
+  float p[PL];
+  float m = -__builtin_inff();
+#pragma unroll
+  for (int j = 0; j < PL; ++j) {
+    const int e = lane + 64 * j;
+    p[j] = e < E ? to_f<DT>(row[e]) : -__builtin_inff();
+    m = fmaxf(m, p[j]);
+  }
+  m = wave_max(m);
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < PL; ++j) {
+    const int e = lane + 64 * j;
+    p[j] = e < E ? iq_expf(p[j] - m) : 0.f;
+    s += p[j];
+  }
+  s = wave_sum(s);
+  // probabilities in the logits' dtype; -1 marks padding and taken entries
+#pragma unroll
+  for (int j = 0; j < PL; ++j) {
+    const int e = lane + 64 * j;
+    p[j] = e < E ? to_f<DT>(from_f<DT>(p[j] / s)) : -1.f;
+  }
+  float mine = 0.f;  // lane i keeps slot i's probability / expert
+  int myexp = 0;
+  float tot = 0.f;
+  for (int i = 0; i < k; ++i) {
+    // lane-local best: largest p, then lowest expert id
+    float bv = -1.f;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int j = 0; j < PL; ++j) {
+      const int e = lane + 64 * j;
+      if (p[j] > bv) { bv = p[j]; bi = e; }  // ascending e within a lane: ties keep the first
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+      const float ov = __shfl_xor(bv, off, 64);
+      const int oi = __shfl_xor(bi, off, 64);
+      if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+    }
+    if ((bi & 63) == lane) {
+#pragma unroll
+      for (int j = 0; j < PL; ++j)
+        if (lane + 64 * j == bi) p[j] = -1.f;
+    }
+    if (lane == i) { mine = bv; myexp = bi; }
+    tot += bv;  // slot order, fp32
+  }
+  if (lane < k) {
+    float v = mine;
+    if (norm) {
+      const float den = to_f<DT>(from_f<DT>(tot));
+      v = to_f<DT>(from_f<DT>(mine / den));
+    }
+    // no candidate left (NaN logits): an invalid expert that combine skips
+    scores[static_cast<int64_t>(t) * k + lane] = mine >= 0.f ? v : __builtin_nanf("");
+    experts[static_cast<int64_t>(t) * k + lane] = mine >= 0.f ? myexp : -1;
+  }
+}
+
+// one workgroup; np = power of two >= n; keys expert' * n + row, where
+// expert' = expert for ids in [0, E) and E otherwise (sorted last)
+__global__ __launch_bounds__(1024) void moe_sort_kernel(const int32_t* experts, int n, int k, int E, int np,
+                                                        int32_t* tokens, int32_t* sorted, int32_t* inverse,
+                                                        int32_t* offsets) {
+  extern __shared__ uint32_t keys[];
+  const int tid = threadIdx.x;
+  for (int i = tid; i < np; i += 1024) {
+    uint32_t key = 0xffffffffu;
+    if (i < n) {
+      const int e = experts[i];
+      const uint32_t ee = (e >= 0 && e < E) ? static_cast<uint32_t>(e) : static_cast<uint32_t>(E);
+      key = ee * static_cast<uint32_t>(n) + static_cast<uint32_t>(i);
+    }
+    keys[i] = key;
+  }
+  for (int size = 2; size <= np; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      __syncthreads();
+      for (int i = tid; i < (np >> 1); i += 1024) {
+        const int lo = 2 * i - (i & (stride - 1));
+        const int hi = lo + stride;
+        const bool asc = (lo & size) == 0;
+        const uint32_t a = keys[lo], b = keys[hi];
+        if ((a > b) == asc) { keys[lo] = b; keys[hi] = a; }
+      }
+    }
+  }
+  __syncthreads();
+  const uint32_t un = static_cast<uint32_t>(n);
+  for (int i = tid; i <= n; i += 1024) {
+    const int ei = i < n ? static_cast<int>(keys[i] / un) : E + 1;
+    if (i < n) {
+      const int r = static_cast<int>(keys[i] % un);
+      tokens[i] = r / k;
+      sorted[i] = experts[r];
+      inverse[r] = i;
+    }
+    if (offsets) {
+      const int ep = i > 0 ? static_cast<int>(keys[i - 1] / un) : -1;
+      for (int e = ep + 1; e <= min(ei, E); ++e) offsets[e] = i;
+    }
+  }
+}
+
+// out[t, d] = sum over t's valid slots in ascending sorted position (=
+// ascending expert) of float(y[pos, d]) * score
+template <int DT>
+__global__ __launch_bounds__(256) void moe_combine_kernel(const typename Store<DT>::T* y, const int32_t* inverse,
+                                                          const int32_t* experts, const float* scores, float* out,
+                                                          int T, int k, int64_t D, int E, int64_t n) {
+  const int64_t d = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (d >= D) return;
+  for (int t = blockIdx.y; t < T; t += gridDim.y) {
+    const int64_t base = static_cast<int64_t>(t) * k;
+    float acc = 0.f;
+    bool first = true;
+    int prev = -1;
+    for (int it = 0; it < k; ++it) {
+      // next slot: smallest sorted position above prev
+      int best = 0x7fffffff, bs = -1;
+      for (int sl = 0; sl < k; ++sl) {
+        const int pos = inverse[base + sl];
+        if (pos > prev && pos < best && pos < n) { best = pos; bs = sl; }  // rows outside y are skipped
+      }
+      if (bs < 0) break;
+      prev = best;
+      const int e = experts[base + bs];
+      if (e < 0 || e >= E) continue;
+      const float v = to_f<DT>(y[static_cast<int64_t>(best) * D + d]) * scores[base + bs];
+      acc = first ? v : acc + v;
+      first = false;
+    }
+    out[static_cast<int64_t>(t) * D + d] = acc;
+  }
+}
+
+template <int DT>
+hipError_t route_pl(const void* logits, float* scores, int32_t* experts, int T, int E, int k, bool norm,
+                    hipStream_t st) {
+  using S = typename Store<DT>::T;
+  const dim3 grid(static_cast<unsigned>((T + 3) / 4));
+  const S* lg = static_cast<const S*>(logits);
+  const int pl = (E + 63) / 64;
+#define IQMM_R(P) \
+  hipLaunchKernelGGL((moe_route_kernel<DT, P>), grid, dim3(256), 0, st, lg, scores, experts, T, E, k, norm ? 1 : 0)
+  if (pl <= 1) IQMM_R(1);
+  else if (pl <= 2) IQMM_R(2);
+  else if (pl <= 4) IQMM_R(4);
+  else if (pl <= 8) IQMM_R(8);
+  else if (pl <= 16) IQMM_R(16);
+  else IQMM_R(32);
+#undef IQMM_R
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_moe_route(const void* logits, int dt, float* scores, int32_t* experts, int T, int E, int k,
+                            bool norm, hipStream_t st) {
+  if (T == 0) return hipSuccess;
+  switch (dt) {
+    case F32: return route_pl<F32>(logits, scores, experts, T, E, k, norm, st);
+    case F16: return route_pl<F16>(logits, scores, experts, T, E, k, norm, st);
+    case BF16: return route_pl<BF16>(logits, scores, experts, T, E, k, norm, st);
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_moe_sort(const int32_t* experts, int n, int k, int E, int32_t* tokens, int32_t* sorted,
+                           int32_t* inverse, int32_t* offsets, hipStream_t st) {
+  int np = 2;
+  while (np < n) np <<= 1;
+  const size_t lds = static_cast<size_t>(np) * 4;
+  if (lds > 65536) {
+    static std::atomic<uint64_t> done{0};  // attribute raised once per device id < 64
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = 64;
+    const uint64_t bit = dev < 64 ? (1ull << dev) : 0;
+    if (!bit || !(done.load(std::memory_order_acquire) & bit)) {
+      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(moe_sort_kernel),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, 131072);
+      if (e != hipSuccess) return e;
+      if (bit) done.fetch_or(bit, std::memory_order_release);
+    }
+  }
+  hipLaunchKernelGGL(moe_sort_kernel, dim3(1), dim3(1024), lds, st, experts, n, k, E, np, tokens, sorted, inverse,
+                     offsets);
+  return hipGetLastError();
+}
+
+hipError_t launch_moe_combine(const void* y, int dt, const int32_t* inverse, const int32_t* experts,
+                              const float* scores, float* out, int T, int k, int64_t D, int E, int64_t n,
+                              hipStream_t st) {
+  if (T == 0 || D == 0) return hipSuccess;
+  const dim3 grid(static_cast<unsigned>((D + 255) / 256), static_cast<unsigned>(T < 65535 ? T : 65535));
+  switch (dt) {
+    case F32:
+      hipLaunchKernelGGL(moe_combine_kernel<F32>, grid, dim3(256), 0, st, static_cast<const float*>(y), inverse,
+                         experts, scores, out, T, k, D, E, n);
+      break;
+    case F16:
+      hipLaunchKernelGGL(moe_combine_kernel<F16>, grid, dim3(256), 0, st, static_cast<const uint16_t*>(y), inverse,
+                         experts, scores, out, T, k, D, E, n);
+      break;
+    case BF16:
+      hipLaunchKernelGGL(moe_combine_kernel<BF16>, grid, dim3(256), 0, st, static_cast<const uint16_t*>(y), inverse,
+                         experts, scores, out, T, k, D, E, n);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace iqmm

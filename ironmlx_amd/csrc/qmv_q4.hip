@@ -163,20 +163,26 @@ struct Q4Args {
   int64_t x_mat, w_mat, s_mat;  // byte strides between batch elements
 };
 
-template <int XT, int RB, int CPL, bool MAPPED, int MR, int MODE = AFFINE>
+//
+// GLU: the weight holds 2N rows (gate rows [0, N), up rows [N, 2N), the fused
+// gate_up layout); a wave reduces RB / 2 gate rows and the matching up rows
+// and writes RB / 2 SwiGLU outputs.
+template <int XT, int RB, int CPL, bool MAPPED, int MR, int MODE = AFFINE, bool GLU = false>
 __global__ __launch_bounds__(64) void qmv_q4_kernel(Q4Args p, BatchMap bm, int64_t batch0) {
+  static_assert(!GLU || (MR == 1 && RB % 2 == 0), "GLU pairs gate / up rows at M = 1");
+  constexpr int RO = GLU ? RB / 2 : RB;  // outputs per wave
   using XS = uint16_t;
   const int lane = threadIdx.x;
   const int64_t bb = batch0 + blockIdx.y;
   const int N = p.N, K = p.K, C = K >> 5;
   XS* out = reinterpret_cast<XS*>(p.out) + bb * static_cast<int64_t>(N) * MR;
-  const int row0 = blockIdx.x * RB;
+  const int row0 = blockIdx.x * RO;
 
   int64_t xi = bb, wi = bb;
   if constexpr (MAPPED) {
     if (!map_batch(bm, bb, xi, wi)) {
-      if (lane < RB * MR && row0 + lane % RB < N)
-        out[static_cast<int64_t>(lane / RB) * N + row0 + lane % RB] = from_f<XT>(__builtin_nanf(""));
+      if (lane < RO * MR && row0 + lane % RO < N)
+        out[static_cast<int64_t>(lane / RO) * N + row0 + lane % RO] = from_f<XT>(__builtin_nanf(""));
       return;
     }
   }
@@ -218,7 +224,9 @@ __global__ __launch_bounds__(64) void qmv_q4_kernel(Q4Args p, BatchMap bm, int64
   XS sr[RB][CPL], br[RB][CPL];
 #pragma unroll
   for (int r = 0; r < RB; ++r) {
-    const uint32_t row = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(min(row0 + r, N - 1)));
+    const int wrow_i = GLU ? (r < RO ? min(row0 + r, N - 1) : N + min(row0 + r - RO, N - 1))
+                           : min(row0 + r, N - 1);
+    const uint32_t row = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(wrow_i));
     const char* wr = w + row * wrow;
     const char* sr_ = sp + row * srow;
     const char* br_ = bp + row * srow;
@@ -267,6 +275,7 @@ __global__ __launch_bounds__(64) void qmv_q4_kernel(Q4Args p, BatchMap bm, int64
       if (lane + 64 * j >= C) xs[m][j] = 0.f;  // masked slot contributes nothing
     }
   // 4. rows in load order
+  float red[RB];  // GLU: reduced sums, valid in lane 63
 #pragma unroll
   for (int r = 0; r < RB; ++r) {
     float acc[MR];
@@ -313,8 +322,14 @@ __global__ __launch_bounds__(64) void qmv_q4_kernel(Q4Args p, BatchMap bm, int64
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
       const float v = dpp_sum_to_lane63(acc[m]);
-      if (lane == 63 && row0 + r < N) out[static_cast<int64_t>(m) * N + row0 + r] = from_f<XT>(v);
+      if constexpr (GLU) red[r] = v;
+      else if (lane == 63 && row0 + r < N) out[static_cast<int64_t>(m) * N + row0 + r] = from_f<XT>(v);
     }
+  }
+  if constexpr (GLU) {
+#pragma unroll
+    for (int o = 0; o < RO; ++o)
+      if (lane == 63 && row0 + o < N) out[row0 + o] = swiglu_out<XT>(red[o], red[RO + o]);
   }
 }
 
@@ -327,24 +342,27 @@ bool qmv_q4_m1_supported(const QmmArgs& a) {
   const int cpl = ((a.K >> 5) + 63) / 64;
   // mxfp4 / nvfp4 (e2m1 codes, one or two byte scales per chunk) at M = 1
   const bool mode_ok = a.mode == AFFINE ? a.bits == 4 : (a.mode == MXFP4 || a.mode == NVFP4) && a.M == 1;
-  return a.transpose && a.M >= 1 && a.M <= 3 && a.M * cpl <= 8 && mode_ok &&
+  // GLU (fused gate / up rows, 2N weight rows) at M = 1 only
+  const int64_t wrows = a.glu ? 2 * static_cast<int64_t>(a.N) : a.N;
+  return a.transpose && a.M >= 1 && a.M <= 3 && a.M * cpl <= 8 && mode_ok && (!a.glu || a.M == 1) &&
          (a.xdt == BF16 || a.xdt == F16) && a.K >= 1024 && a.K <= 16384 &&
-         static_cast<int64_t>(a.N) * (a.K / 2) < (int64_t{1} << 32);
+         wrows * (a.K / 2) < (int64_t{1} << 32);
 }
 
 namespace {
-template <int XT, int RB, int CPL, int MR, int MODE = AFFINE>
+template <int XT, int RB, int CPL, int MR, int MODE = AFFINE, bool GLU = false>
 void launch_mr(dim3 grid, const QmmArgs& a, const Q4Args& p, bool mapped, int64_t b0) {
-  if constexpr (MR * CPL > 8) return;  // excluded by qmv_q4_m1_supported
+  if constexpr (MR * CPL > 8 || (GLU && (MR != 1 || RB % 2 != 0))) return;  // excluded by the callers
   else if (mapped)
-    hipLaunchKernelGGL((qmv_q4_kernel<XT, RB, CPL, true, MR, MODE>), grid, dim3(64), 0, a.stream, p, a.bm, b0);
+    hipLaunchKernelGGL((qmv_q4_kernel<XT, RB, CPL, true, MR, MODE, GLU>), grid, dim3(64), 0, a.stream, p, a.bm, b0);
   else
-    hipLaunchKernelGGL((qmv_q4_kernel<XT, RB, CPL, false, MR, MODE>), grid, dim3(64), 0, a.stream, p, a.bm, b0);
+    hipLaunchKernelGGL((qmv_q4_kernel<XT, RB, CPL, false, MR, MODE, GLU>), grid, dim3(64), 0, a.stream, p, a.bm, b0);
 }
 
 template <int XT, int RB, int CPL>
 hipError_t launch_ord(const QmmArgs& a) {
-  const int64_t nrb = (a.N + RB - 1) / RB;
+  const int ro = a.glu ? RB / 2 : RB;  // outputs per wave
+  const int64_t nrb = (a.N + ro - 1) / ro;
   if (nrb <= 0 || a.nbatch <= 0) return hipSuccess;
   Q4Args p;
   p.x = static_cast<const char*>(a.x);
@@ -363,6 +381,12 @@ hipError_t launch_ord(const QmmArgs& a) {
   for (int64_t b0 = 0; b0 < a.nbatch; b0 += 65535) {
     const int64_t nb = a.nbatch - b0 < 65535 ? a.nbatch - b0 : 65535;
     const dim3 grid(static_cast<unsigned>(nrb), static_cast<unsigned>(nb));
+    if (a.glu) {
+      if (a.mode == MXFP4) launch_mr<XT, RB, CPL, 1, MXFP4, true>(grid, a, p, mapped, b0);
+      else if (a.mode == NVFP4) launch_mr<XT, RB, CPL, 1, NVFP4, true>(grid, a, p, mapped, b0);
+      else launch_mr<XT, RB, CPL, 1, AFFINE, true>(grid, a, p, mapped, b0);
+      continue;
+    }
     if (a.mode == MXFP4) { launch_mr<XT, RB, CPL, 1, MXFP4>(grid, a, p, mapped, b0); continue; }
     if (a.mode == NVFP4) { launch_mr<XT, RB, CPL, 1, NVFP4>(grid, a, p, mapped, b0); continue; }
     switch (a.M) {
@@ -379,9 +403,10 @@ hipError_t launch_ord_cpl(const QmmArgs& a) {
   // rows per wave (measured on MI355X): 2 from 4096 rows, 4 from 24576 rows
   // (x and the per-chunk setup amortize over more rows once the grid is
   // large), 1 below 4096 rows so small matrices still spread over the CUs
-  const int64_t rows = a.N * a.nbatch;
+  const int64_t rows = static_cast<int64_t>(a.glu ? 2 * a.N : a.N) * a.nbatch;
   int rb = rows >= 24576 ? 4 : rows >= 4096 ? 2 : 1;
   if (CPL >= 4 && rb > 2) rb = 2;
+  if (a.glu && rb < 2) rb = 2;  // a gate row and its up row per output
   switch (rb) {
     case 4: return launch_ord<XT, 4, CPL>(a);
     case 2: return launch_ord<XT, 2, CPL>(a);

@@ -7,15 +7,20 @@ These are the reference's users of the drop-in boundary, restated over
 * :class:`QuantizedLinear`, :class:`LinearLayer` -- mlx/src/nn/linear.rs:9-157
 * :class:`QuantizedEmbedding`  -- mlx/src/nn/embedding.rs:39-96
 * :class:`MLP` / :class:`Expert` (SwiGLU) -- mlx/src/nn/mlp.rs:11-33,
-  mlx/src/nn/moe.rs:10-33
+  mlx/src/nn/moe.rs:10-33; :class:`FusedMLP` runs gate and up as one fused
+  SwiGLU call over a stacked gate_up weight
 * :func:`split_fused_experts`  -- the fused gate_up_proj split of
   mlx/src/model/qwen35.rs:591-778, kept as stacked [E, N, K/pack] tensors
+* :func:`stack_fused_experts` -- the same tensors kept unsplit for the fused
+  gate_up SwiGLU gather
 * :class:`MoEMLP`              -- mlx/src/nn/moe.rs:55-183, with the
-  per-expert host loop replaced by two sorted :func:`ops.gather_qmm` passes
+  per-expert host loop replaced by sorted :func:`ops.gather_qmm` passes and
+  the routing (softmax / top-k / normalise, the sort by expert, the weighted
+  combine) run on the device by the library
 
-The quantized products run in libiqmm.so.  Routing (softmax / top-k), the
-SwiGLU elementwise step, the dense router and the weighted combine use torch
-device ops; they are outside the quantized path.
+The quantized products and the routing run in libiqmm.so.  The dense router
+and shared-expert gate (plain Linear) and the unfused SwiGLU step of
+:class:`MLP` use torch device ops; they are outside the quantized path.
 """
 from __future__ import annotations
 
@@ -110,9 +115,11 @@ class QuantizedEmbedding:
         self.group_size, self.bits, self.mode = group_size, bits, mode
 
     def __call__(self, tokens: torch.Tensor, stream=None) -> torch.Tensor:
-        table = ops.dequantize(self.weight, self.scales, self.biases, self.group_size, self.bits,
-                               self.mode, stream)
-        return table.index_select(0, tokens.reshape(-1).long()).reshape(*tokens.shape, -1)
+        """Rows of dequantize(table) for the token ids, gathered without
+        dequantizing the whole table (bit-identical to embedding.rs:62-72)."""
+        idx = tokens if tokens.dtype in (torch.int32, torch.int64) else tokens.long()
+        return ops.dequantize_rows(self.weight, self.scales, self.biases, idx.contiguous(),
+                                   self.group_size, self.bits, self.mode, stream)
 
     def as_linear(self, x: torch.Tensor, stream=None) -> torch.Tensor:
         """Tied lm_head: x @ dequant(table)^T (llama.rs:158-162)."""
@@ -133,6 +140,34 @@ class MLP:
 
 
 Expert = MLP  # moe.rs:10-33 has the same composition
+
+
+class FusedMLP:
+    """down(silu(gate(x)) * up(x)) with gate and up stacked into one
+    [2I, K/pack] weight (gate rows first) and evaluated by one fused SwiGLU
+    call: x is read once and the elementwise step runs in the product's
+    epilogue (one launch at decode).  Same rounding as :class:`MLP`."""
+
+    def __init__(self, gate_up: QuantizedLinear, down_proj):
+        self.gate_up, self.down_proj = gate_up, down_proj
+
+    @classmethod
+    def from_mlp(cls, mlp: MLP) -> "FusedMLP":
+        g, u = mlp.gate_proj, mlp.up_proj
+        if not (isinstance(g, QuantizedLinear) and isinstance(u, QuantizedLinear)):
+            raise TypeError("FusedMLP needs quantized gate and up projections")
+        if (g.group_size, g.bits, g.mode) != (u.group_size, u.bits, u.mode):
+            raise ValueError("gate and up must share group_size, bits and mode")
+        cat = lambda a, b: None if a is None else torch.cat([a, b], dim=0).contiguous()
+        gu = QuantizedLinear(cat(g.weight, u.weight), cat(g.scales, u.scales),
+                             cat(g.biases, u.biases), g.group_size, g.bits, g.mode)
+        return cls(gu, mlp.down_proj)
+
+    def __call__(self, x, stream=None):
+        gu = self.gate_up
+        h = ops.quantized_swiglu(x, gu.weight, gu.scales, gu.biases, gu.group_size, gu.bits,
+                                 gu.mode, stream)
+        return self.down_proj(h, stream)
 
 
 @dataclass
@@ -174,8 +209,24 @@ def split_fused_experts(weights: Dict[str, torch.Tensor], prefix: str, group_siz
     return out
 
 
-def _gqmm(x, e: StackedExperts, rhs, sorted_indices=True, stream=None):
-    return ops.gather_qmm(x, e.weight, e.scales, e.biases, None, rhs, True, e.group_size, e.bits,
+def stack_fused_experts(weights: Dict[str, torch.Tensor], prefix: str, group_size=64, bits=4,
+                        mode="affine") -> Dict[str, StackedExperts]:
+    """The expert tensors of qwen35.rs:655-775 kept as loaded: the fused
+    gate_up_proj [E, 2I, .] (gate rows first) for :func:`ops.gather_qmm_swiglu`
+    and down_proj [E, H, .]; no copies."""
+    base = f"{prefix}.mlp.experts"
+    return {
+        "gate_up": StackedExperts(weights[f"{base}.gate_up_proj.weight"],
+                                  weights[f"{base}.gate_up_proj.scales"],
+                                  weights.get(f"{base}.gate_up_proj.biases"), group_size, bits, mode),
+        "down": StackedExperts(weights[f"{base}.down_proj.weight"],
+                               weights[f"{base}.down_proj.scales"],
+                               weights.get(f"{base}.down_proj.biases"), group_size, bits, mode),
+    }
+
+
+def _gqmm(x, e: StackedExperts, rhs, lhs=None, sorted_indices=True, stream=None):
+    return ops.gather_qmm(x, e.weight, e.scales, e.biases, lhs, rhs, True, e.group_size, e.bits,
                           e.mode, sorted_indices, stream)
 
 
@@ -184,9 +235,12 @@ class MoEMLP:
     -> weighted sum, plus a sigmoid-gated shared expert (moe.rs:55-183).
 
     The reference evaluates routing on the host and runs one quantized_matmul
-    per used expert per projection (moe.rs:86-143); here the (token, slot)
-    rows are sorted by expert on the device and each projection is a single
-    sorted gather_qmm over the stacked expert tensors."""
+    per used expert per projection (moe.rs:86-143); here routing, the sort of
+    the (token, slot) rows by expert and the weighted combine run on the
+    device (no host synchronisation), and each projection is a single sorted
+    gather_qmm over the stacked expert tensors -- with ``experts["gate_up"]``
+    (:func:`stack_fused_experts`) gate, up and the SwiGLU are one fused call.
+    Like the reference (moe.rs:146-172), the result is float32."""
 
     def __init__(self, gate: Linear, experts: Dict[str, StackedExperts], shared_expert: MLP,
                  shared_expert_gate: Linear, num_experts_per_tok: int, norm_topk_prob: bool = True):
@@ -194,34 +248,36 @@ class MoEMLP:
         self.shared_expert, self.shared_expert_gate = shared_expert, shared_expert_gate
         self.k, self.norm_topk_prob = num_experts_per_tok, norm_topk_prob
 
-    def route(self, x_flat):
-        logits = self.gate(x_flat)
-        probs = torch.softmax(logits.float(), dim=-1)
-        scores, idx = torch.topk(probs, self.k, dim=-1)
-        if self.norm_topk_prob:
-            scores = scores / scores.sum(-1, keepdim=True)
-        return scores, idx
+    def num_experts(self) -> int:
+        return int(self.experts["down"].weight.shape[0])
+
+    def route(self, x_flat, stream=None):
+        """(scores float32 [T, k], experts int32 [T, k]) (moe.rs:66-82)."""
+        logits = self.gate(x_flat).contiguous()
+        return ops.moe_route(logits, self.k, self.norm_topk_prob, stream)
 
     def experts_forward(self, x_flat, scores, idx, stream=None):
         n, d = x_flat.shape
-        flat = idx.reshape(-1)
-        order = torch.argsort(flat, stable=True)
-        rhs = flat[order].to(torch.int32).contiguous()
-        xs = x_flat[order // self.k].reshape(n * self.k, 1, d).contiguous()
-        g = _gqmm(xs, self.experts["gate"], rhs, stream=stream)
-        u = _gqmm(xs, self.experts["up"], rhs, stream=stream)
-        h = (F.silu(g) * u).contiguous()
-        y = _gqmm(h, self.experts["down"], rhs, stream=stream).reshape(n * self.k, -1)
-        w = scores.reshape(-1)[order].to(y.dtype).unsqueeze(-1)
-        out = torch.zeros((n, y.shape[-1]), dtype=torch.float32, device=y.device)
-        out.index_add_(0, order // self.k, (y * w).float())
-        return out.to(x_flat.dtype)
+        E = self.num_experts()
+        idx = idx.to(torch.int32).contiguous()
+        tokens, rhs, inverse, _ = ops.moe_sort(idx, E, stream)
+        x3 = x_flat.reshape(n, 1, d).contiguous()
+        if "gate_up" in self.experts:
+            gu = self.experts["gate_up"]
+            h = ops.gather_qmm_swiglu(x3, gu.weight, gu.scales, gu.biases, tokens, rhs,
+                                      gu.group_size, gu.bits, gu.mode, True, stream)
+        else:
+            g = _gqmm(x3, self.experts["gate"], rhs, tokens, stream=stream)
+            u = _gqmm(x3, self.experts["up"], rhs, tokens, stream=stream)
+            h = (F.silu(g) * u).contiguous()
+        y = _gqmm(h, self.experts["down"], rhs, stream=stream)
+        return ops.moe_combine(y, inverse, idx, scores.contiguous(), E, stream)
 
     def __call__(self, x, stream=None):
         b, l, d = x.shape
         x_flat = x.reshape(b * l, d)
-        scores, idx = self.route(x_flat)
+        scores, idx = self.route(x_flat, stream)
         out = self.experts_forward(x_flat, scores, idx, stream)
         shared = self.shared_expert(x_flat, stream)
         gate = torch.sigmoid(self.shared_expert_gate(x_flat))
-        return (out + shared * gate).reshape(b, l, d)
+        return (out + (shared * gate).float()).reshape(b, l, d)

@@ -140,6 +140,93 @@ def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
     return _run(L.iqmm_gather_qmm, _lib.IqmmArray(), dev, args)
 
 
+def quantized_swiglu(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
+                     biases: Optional[torch.Tensor] = None, group_size: Optional[int] = None,
+                     bits: Optional[int] = None, mode: str = "affine", stream=None) -> torch.Tensor:
+    """``silu(x @ gate^T) * (x @ up^T)`` over a fused gate_up weight (gate rows
+    first, then up rows): the gate / up / silu / multiply of
+    ``MLP::forward_with_stream`` (mlx/src/nn/mlp.rs:27-33) in one call."""
+    L = _lib.load()
+    dev = _device_of(x, w, scales, biases)
+    args = (_arr(x), _arr(w, True), _arr(scales), _arr(biases), _lib.opt_int(group_size),
+            _lib.opt_int(bits), _mode(mode), _stream(dev, stream))
+    return _run(L.iqmm_quantized_swiglu, _lib.IqmmArray(), dev, args)
+
+
+def gather_qmm_swiglu(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
+                      biases: Optional[torch.Tensor] = None,
+                      lhs_indices: Optional[torch.Tensor] = None,
+                      rhs_indices: Optional[torch.Tensor] = None,
+                      group_size: Optional[int] = None, bits: Optional[int] = None,
+                      mode: str = "affine", sorted_indices: bool = False,
+                      stream=None) -> torch.Tensor:
+    """:func:`gather_qmm` over stacked gate_up experts [E, 2I, .] followed by
+    the SwiGLU of :func:`quantized_swiglu` (each Expert of mlx/src/nn/moe.rs:10-33)."""
+    L = _lib.load()
+    dev = _device_of(x, w, scales, biases, lhs_indices, rhs_indices)
+    args = (_arr(x), _arr(w, True), _arr(scales), _arr(biases), _arr(lhs_indices),
+            _arr(rhs_indices), _lib.opt_int(group_size), _lib.opt_int(bits), _mode(mode),
+            bool(sorted_indices), _stream(dev, stream))
+    return _run(L.iqmm_gather_qmm_swiglu, _lib.IqmmArray(), dev, args)
+
+
+def dequantize_rows(w: torch.Tensor, scales: torch.Tensor, biases: Optional[torch.Tensor],
+                    indices: torch.Tensor, group_size: Optional[int] = None,
+                    bits: Optional[int] = None, mode: str = "affine", stream=None,
+                    dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """``dequantize(w)[indices]`` without dequantizing the table (the lookup of
+    ``QuantizedEmbedding::forward``, mlx/src/nn/embedding.rs:62-72)."""
+    L = _lib.load()
+    dev = _device_of(w, scales, biases, indices)
+    od = _lib.OptionalDtype(0, False) if dtype is None else \
+        _lib.OptionalDtype(_TORCH_TO_DT[dtype], True)
+    args = (_arr(w, True), _arr(scales), _arr(biases), _arr(indices), _lib.opt_int(group_size),
+            _lib.opt_int(bits), _mode(mode), od, _stream(dev, stream))
+    return _run(L.iqmm_dequantize_rows, _lib.IqmmArray(), dev, args)
+
+
+def _run_multi(fn, n_out: int, dev, args, optional_last: bool = False):
+    res = [_lib.IqmmArray() for _ in range(n_out)]
+    refs = [ctypes.byref(r) for r in res]
+    _lib.check(fn(*refs, *args))
+    outs = [_alloc(r, dev) for r in res]
+    for r, t in zip(res, outs):
+        r.data = t.data_ptr() or 1
+    _lib.check(fn(*refs, *args))
+    return outs
+
+
+def moe_route(logits: torch.Tensor, k: int, norm_topk_prob: bool = True,
+              stream=None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Softmax over experts, top-k (stable descending), optional normalisation
+    (mlx/src/nn/moe.rs:67-82).  Returns (scores float32 [T, k], experts int32 [T, k])."""
+    L = _lib.load()
+    dev = _device_of(logits)
+    args = (_arr(logits), int(k), bool(norm_topk_prob), _stream(dev, stream))
+    scores, experts = _run_multi(L.iqmm_moe_route, 2, dev, args)
+    return scores, experts
+
+
+def moe_sort(experts: torch.Tensor, num_experts: int, stream=None):
+    """Stable sort of the (token, slot) rows by expert (mlx/src/nn/moe.rs:92-104).
+    Returns (tokens, sorted_experts, inverse, offsets), all int32."""
+    L = _lib.load()
+    dev = _device_of(experts)
+    args = (_arr(experts), int(num_experts), _stream(dev, stream))
+    return tuple(_run_multi(L.iqmm_moe_sort, 4, dev, args))
+
+
+def moe_combine(y: torch.Tensor, inverse: torch.Tensor, experts: torch.Tensor,
+                scores: torch.Tensor, num_experts: int, stream=None) -> torch.Tensor:
+    """Per token, the sorted expert rows times their scores summed in float32 in
+    ascending expert order (mlx/src/nn/moe.rs:146-168).  Returns float32 [T, D]."""
+    L = _lib.load()
+    dev = _device_of(y, inverse, experts, scores)
+    args = (_arr(y), _arr(inverse), _arr(experts), _arr(scores), int(num_experts),
+            _stream(dev, stream))
+    return _run(L.iqmm_moe_combine, _lib.IqmmArray(), dev, args)
+
+
 def quantize(w: torch.Tensor, group_size: Optional[int] = None, bits: Optional[int] = None,
              mode: str = "affine", stream=None
              ) -> Tuple[torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
@@ -161,4 +248,6 @@ def quantize(w: torch.Tensor, group_size: Optional[int] = None, bits: Optional[i
     return tw, ts, tb
 
 
-__all__ = ["quantized_matmul", "dequantize", "gather_qmm", "quantize", "IqmmError"]
+__all__ = ["quantized_matmul", "dequantize", "gather_qmm", "quantize", "quantized_swiglu",
+           "gather_qmm_swiglu", "dequantize_rows", "moe_route", "moe_sort", "moe_combine",
+           "IqmmError"]

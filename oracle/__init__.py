@@ -27,6 +27,17 @@ Parity status of each function (how it is pinned, see tests/test_oracle.py):
     block scale = RNE(amax/6), each element the nearest grid point by brute
     force).  MLX's own tie/eps/scale-selection choices for quantize are not
     verifiable without MLX: "parity unpinned" against MLX itself.
+  * expf: pinned against float64 exp (<= 2 ulp over the float range) and
+    exact points (exp(0) = 1, overflow / underflow edges).
+  * swiglu: pinned by closed forms (g = 0 gives 0, saturated sigmoid gives
+    rn(g * u), large negative g gives 0) and float64 silu(g)*u within the
+    rounding of its three steps.  MLX's own sigmoid rounding: "parity
+    unpinned" against MLX itself.
+  * moe_route: pinned by float64 softmax + numpy stable argsort on
+    well-separated logits (exact ids), tie cases (lower id first) and
+    normalised scores summing to 1.
+  * moe_sort: pinned by numpy stable argsort of the expert ids.
+  * moe_combine: pinned by float64 weighted sums and the k = 1 identity.
 """
 from __future__ import annotations
 
@@ -85,6 +96,12 @@ def lib():
         L.iqo_fp_quantize.argtypes = [vp, i32, i64, i64, i32, vp, vp]
         L.iqo_from_float_array.argtypes = [vp, i64, i32, vp]
         L.iqo_to_float_array.argtypes = [vp, i64, i32, vp]
+        L.iqo_expf.restype = ctypes.c_float
+        L.iqo_expf.argtypes = [ctypes.c_float]
+        L.iqo_swiglu.argtypes = [vp, i32, i64, i64, vp]
+        L.iqo_moe_route.argtypes = [vp, i32, i64, i64, i32, i32, vp, vp]
+        L.iqo_moe_sort.argtypes = [vp, i64, i32, i32, vp, vp, vp, vp]
+        L.iqo_moe_combine.argtypes = [vp, i32, i64, vp, vp, vp, i64, i32, i32, vp]
         _lib = L
     return _lib
 
@@ -232,3 +249,53 @@ def fp_quantize(w, wdt, mode):
     sc = np.zeros((rows, K // gs), np.uint8)
     lib().iqo_fp_quantize(_p(w), DT[wdt], rows, K, MODES[mode], _p(wq), _p(sc))
     return wq, sc
+
+
+# ----------------------------------------------------------------- SwiGLU / MoE routing
+def expf(x) -> np.ndarray:
+    """The library's exp restated (Cody-Waite + degree-7 Taylor, float32)."""
+    x = _c(x, np.float32)
+    L = lib()
+    return np.array([L.iqo_expf(float(v)) for v in x.ravel()], np.float32).reshape(x.shape)
+
+
+def swiglu(gu, dt: str) -> np.ndarray:
+    """gu [rows, 2I] (gate | up, tagged dt) -> silu(gate) * up [rows, I], each
+    elementwise step rounded to dt (mlx/src/nn/mlp.rs:27-33)."""
+    gu = _c(gu, NP_STORAGE[dt])
+    rows, two_i = gu.shape
+    out = np.zeros((rows, two_i // 2), NP_STORAGE[dt])
+    lib().iqo_swiglu(_p(gu), DT[dt], rows, two_i // 2, _p(out))
+    return out
+
+
+def moe_route(logits, dt: str, k: int, norm: bool = True):
+    """logits [T, E] -> (scores f32 [T, k], experts i32 [T, k]) (moe.rs:67-82)."""
+    lg = _c(logits, NP_STORAGE[dt])
+    T, E = lg.shape
+    scores = np.zeros((T, k), np.float32)
+    experts = np.zeros((T, k), np.int32)
+    lib().iqo_moe_route(_p(lg), DT[dt], T, E, k, int(norm), _p(scores), _p(experts))
+    return scores, experts
+
+
+def moe_sort(experts, num_experts: int):
+    """experts [T, k] i32 -> (tokens, sorted, inverse, offsets), stable by expert."""
+    ex = _c(experts, np.int32)
+    n, k = ex.size, ex.shape[1]
+    tokens, srt, inv = (np.zeros(n, np.int32) for _ in range(3))
+    offs = np.zeros(num_experts + 1, np.int32)
+    lib().iqo_moe_sort(_p(ex), n, k, num_experts, _p(tokens), _p(srt), _p(inv), _p(offs))
+    return tokens, srt, inv, offs
+
+
+def moe_combine(y, dt: str, inverse, experts, scores, num_experts: int) -> np.ndarray:
+    """y [n, D] sorted expert rows -> float32 [T, D] (moe.rs:146-168)."""
+    y = _c(y, NP_STORAGE[dt])
+    D = y.shape[-1]
+    ex = _c(experts, np.int32)
+    T, k = ex.shape
+    out = np.zeros((T, D), np.float32)
+    lib().iqo_moe_combine(_p(y), DT[dt], D, _p(_c(inverse, np.int32)), _p(ex),
+                          _p(_c(scores, np.float32)), T, k, num_experts, _p(out))
+    return out

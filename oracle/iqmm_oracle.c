@@ -156,6 +156,15 @@ static inline void store_f(void* p, int dt, int64_t i, float v) {
   }
 }
 
+/* value rounded to dt and read back as float */
+static inline float load_round(float v, int dt) {
+  switch (dt) {
+    case IQO_F32: return v;
+    case IQO_F16: return iqo_half_to_float(iqo_float_to_half(v));
+    default: return iqo_bf16_to_float(iqo_float_to_bf16(v));
+  }
+}
+
 /* ------------------------------------------------------------------ */
 /* bit stream                                                          */
 /* ------------------------------------------------------------------ */
@@ -387,4 +396,140 @@ void iqo_from_float_array(const float* in, int64_t n, int dt, void* out) {
 }
 void iqo_to_float_array(const void* in, int64_t n, int dt, float* out) {
   for (int64_t i = 0; i < n; ++i) out[i] = load_f(in, dt, i);
+}
+
+/* ------------------------------------------------------------------ */
+/* SwiGLU and MoE routing (mlx/src/nn/mlp.rs:27-33,                    */
+/* mlx/src/nn/activations.rs:7-10, mlx/src/nn/moe.rs:67-168)           */
+/* ------------------------------------------------------------------ */
+
+/* exp(x) by Cody-Waite reduction x = n ln2 + r (|r| <= ln2 / 2, ln2 split
+ * into a 16-bit head and a tail so n * head is exact) and the degree-7
+ * Taylor polynomial of e^r in Horner form with explicit fmaf, then a 2^n
+ * scale.  Every step is a correctly rounded IEEE operation, so the library's
+ * device copy of these steps gives bit-identical results.  MLX's own exp is
+ * not available here: this function is pinned against float64 exp (<= 2 ulp)
+ * by the tests, not against MLX. */
+float iqo_expf(float x) {
+  if (x != x) return x;
+  if (x > 88.7228394f) return INFINITY;
+  if (x < -103.972084f) return 0.0f;
+  const float n = rintf(x * 1.44269502f);
+  float r = fmaf(-n, 0.693145751953125f, x);
+  r = fmaf(-n, 1.42860682e-6f, r);
+  float p = 1.0f / 5040.0f;
+  p = fmaf(p, r, 1.0f / 720.0f);
+  p = fmaf(p, r, 1.0f / 120.0f);
+  p = fmaf(p, r, 1.0f / 24.0f);
+  p = fmaf(p, r, 1.0f / 6.0f);
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  return ldexpf(p, (int)n);
+}
+
+/* silu(g) * u of stored (rounded) gate / up values, each elementwise op
+ * rounded to dt: s = rn(1 / (1 + exp(-g))), a = rn(g * s), out = rn(a * u). */
+static float swiglu1(float g, float u, int dt) {
+  const float gr = load_round(g, dt), ur = load_round(u, dt);
+  const float sg = load_round(1.0f / (1.0f + iqo_expf(-gr)), dt);
+  const float a = load_round(gr * sg, dt);
+  return a * ur;
+}
+
+/* gu [rows, 2I] (gate | up) -> out [rows, I] */
+void iqo_swiglu(const void* gu, int dt, int64_t rows, int64_t I, void* out) {
+  for (int64_t r = 0; r < rows; ++r)
+    for (int64_t c = 0; c < I; ++c)
+      store_f(out, dt, r * I + c, swiglu1(load_f(gu, dt, r * 2 * I + c), load_f(gu, dt, r * 2 * I + I + c), dt));
+}
+
+/* Router of one token set: softmax over E experts in fp32, the sum taken in
+ * the library's fixed order (64 lane partial sums over e = lane + 64 j in j
+ * order, then a butterfly over lane distances 32, 16, .., 1), probabilities
+ * rounded to dt; the k largest by a stable descending sort (ties: lower id,
+ * as a stable argsort of -p, moe.rs:72-73); with norm, rn(p / rn(sum of the
+ * k in slot order)) (moe.rs:76-82). */
+void iqo_moe_route(const void* logits, int dt, int64_t T, int64_t E, int k, int norm, float* scores,
+                   int32_t* experts) {
+  float* p = (float*)malloc(sizeof(float) * (size_t)E);
+  int32_t* ord = (int32_t*)malloc(sizeof(int32_t) * (size_t)E);
+  float part[64];
+  for (int64_t t = 0; t < T; ++t) {
+    float m = -INFINITY;
+    for (int64_t e = 0; e < E; ++e) {
+      p[e] = load_f(logits, dt, t * E + e);
+      m = fmaxf(m, p[e]);
+    }
+    for (int l = 0; l < 64; ++l) part[l] = 0.0f;
+    for (int64_t e = 0; e < E; ++e) {
+      p[e] = iqo_expf(p[e] - m);
+      part[e % 64] = part[e % 64] + p[e];
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+      float nx[64];
+      for (int l = 0; l < 64; ++l) nx[l] = part[l] + part[l ^ off];
+      memcpy(part, nx, sizeof(nx));
+    }
+    const float s = part[0];
+    for (int64_t e = 0; e < E; ++e) p[e] = load_round(p[e] / s, dt);
+    /* stable insertion sort of ids by descending p */
+    for (int64_t e = 0; e < E; ++e) {
+      int64_t j = e;
+      while (j > 0 && p[ord[j - 1]] < p[e]) { ord[j] = ord[j - 1]; --j; }
+      ord[j] = (int32_t)e;
+    }
+    float tot = 0.0f;
+    for (int i = 0; i < k; ++i) tot = tot + p[ord[i]];
+    for (int i = 0; i < k; ++i) {
+      float v = p[ord[i]];
+      if (norm) v = load_round(v / load_round(tot, dt), dt);
+      scores[t * k + i] = v;
+      experts[t * k + i] = ord[i];
+    }
+  }
+  free(p);
+  free(ord);
+}
+
+/* Stable sort of the n (token, slot) rows by expert; ids outside [0, E)
+ * after all valid ones; offsets[e] = first row of expert e, offsets[E] =
+ * number of valid rows (moe.rs:92-104 builds the same per-expert lists). */
+void iqo_moe_sort(const int32_t* experts, int64_t n, int k, int E, int32_t* tokens, int32_t* sorted,
+                  int32_t* inverse, int32_t* offsets) {
+  int64_t pos = 0;
+  for (int e = 0; e <= E; ++e) {
+    offsets[e] = (int32_t)pos;
+    for (int64_t r = 0; r < n; ++r) {
+      const int32_t x = experts[r];
+      const int valid = x >= 0 && x < E;
+      if ((e < E && valid && x == e) || (e == E && !valid)) {
+        tokens[pos] = (int32_t)(r / k);
+        sorted[pos] = x;
+        inverse[r] = (int32_t)pos;
+        ++pos;
+      }
+    }
+  }
+}
+
+/* out[t, :] = sum over t's slots with a valid expert, in ascending expert
+ * order, of float(y[inverse[slot], :]) * score: the first product as is, each
+ * further one added in fp32 (moe.rs:146-168). */
+void iqo_moe_combine(const void* y, int dt, int64_t D, const int32_t* inverse, const int32_t* experts,
+                     const float* scores, int64_t T, int k, int E, float* out) {
+  for (int64_t t = 0; t < T; ++t) {
+    for (int64_t d = 0; d < D; ++d) {
+      float acc = 0.0f;
+      int first = 1;
+      for (int e = 0; e < E; ++e)
+        for (int s = 0; s < k; ++s)
+          if (experts[t * k + s] == e) {
+            const float v = load_f(y, dt, (int64_t)inverse[t * k + s] * D + d) * scores[t * k + s];
+            acc = first ? v : acc + v;
+            first = 0;
+          }
+      out[t * D + d] = acc;
+    }
+  }
 }

@@ -165,3 +165,65 @@ def test_gather_qmm_query():
                            A((64, 8), F32), True, _lib.opt_int(None), _lib.opt_int(None),
                            b"affine", False, None)
     assert rc != 0 and "integers" in L.iqmm_last_error().decode()
+
+
+# ------------------------------------------------------------------ fused / routing entry points
+def test_swiglu_infer_and_errors():
+    L = _lib.load()
+    res = _lib.IqmmArray()
+    rc = L.iqmm_quantized_swiglu(ctypes.byref(res), A((1, 4096), BF16), A((28672, 512), U32),
+                                 A((28672, 64), BF16), A((28672, 64), BF16), _lib.opt_int(None),
+                                 _lib.opt_int(None), b"affine", None)
+    assert rc == 0, L.iqmm_last_error().decode()
+    assert shape_of(res) == (1, 14336) and res.dtype == BF16
+    res = _lib.IqmmArray()
+    rc = L.iqmm_quantized_swiglu(ctypes.byref(res), A((1, 4096), BF16), A((301, 512), U32),
+                                 A((301, 64), BF16), A((301, 64), BF16), _lib.opt_int(None),
+                                 _lib.opt_int(None), b"affine", None)
+    assert rc != 0 and "even number of rows" in L.iqmm_last_error().decode()
+    res = _lib.IqmmArray()
+    rc = L.iqmm_gather_qmm_swiglu(ctypes.byref(res), A((64, 1, 2048), BF16), A((256, 1024, 256), U32),
+                                  A((256, 1024, 32), BF16), A((256, 1024, 32), BF16), A((512,), I32),
+                                  A((512,), I32), _lib.opt_int(None), _lib.opt_int(None), b"affine", True,
+                                  None)
+    assert rc == 0, L.iqmm_last_error().decode()
+    assert shape_of(res) == (512, 1, 512)
+
+
+def test_dequantize_rows_infer_and_errors():
+    L = _lib.load()
+    od = _lib.OptionalDtype(0, False)
+    res = _lib.IqmmArray()
+    rc = L.iqmm_dequantize_rows(ctypes.byref(res), A((128256, 512), U32), A((128256, 64), BF16),
+                                A((128256, 64), BF16), A((2, 7), I32), _lib.opt_int(None),
+                                _lib.opt_int(None), b"affine", od, None)
+    assert rc == 0, L.iqmm_last_error().decode()
+    assert shape_of(res) == (2, 7, 4096) and res.dtype == BF16
+    res = _lib.IqmmArray()
+    rc = L.iqmm_dequantize_rows(ctypes.byref(res), A((100, 512), U32), A((100, 64), BF16),
+                                A((100, 64), BF16), A((3,), F32), _lib.opt_int(None),
+                                _lib.opt_int(None), b"affine", od, None)
+    assert rc != 0 and "indices must be an integer array" in L.iqmm_last_error().decode()
+
+
+def test_moe_entry_points_infer_and_errors():
+    L = _lib.load()
+    rs, re_ = _lib.IqmmArray(), _lib.IqmmArray()
+    rc = L.iqmm_moe_route(ctypes.byref(rs), ctypes.byref(re_), A((512, 256), BF16), 8, True, None)
+    assert rc == 0, L.iqmm_last_error().decode()
+    assert shape_of(rs) == (512, 8) and rs.dtype == F32 and re_.dtype == I32
+    rs, re_ = _lib.IqmmArray(), _lib.IqmmArray()
+    assert L.iqmm_moe_route(ctypes.byref(rs), ctypes.byref(re_), A((4, 16), BF16), 17, True, None) != 0
+    assert "k must be" in L.iqmm_last_error().decode()
+    outs = [_lib.IqmmArray() for _ in range(4)]
+    rc = L.iqmm_moe_sort(*[ctypes.byref(o) for o in outs], A((512, 8), I32), 256, None)
+    assert rc == 0, L.iqmm_last_error().decode()
+    assert [shape_of(o) for o in outs] == [(4096,), (4096,), (4096,), (257,)]
+    outs = [_lib.IqmmArray() for _ in range(4)]
+    assert L.iqmm_moe_sort(*[ctypes.byref(o) for o in outs], A((5000, 8), I32), 256, None) != 0
+    assert "32768" in L.iqmm_last_error().decode()
+    res = _lib.IqmmArray()
+    rc = L.iqmm_moe_combine(ctypes.byref(res), A((4096, 1, 2048), BF16), A((4096,), I32), A((512, 8), I32),
+                            A((512, 8), F32), 256, None)
+    assert rc == 0, L.iqmm_last_error().decode()
+    assert shape_of(res) == (512, 2048) and res.dtype == F32

@@ -1,6 +1,7 @@
 """GPU checks of the caller layer: QuantizedLinear == quantized_matmul,
-QuantizedEmbedding == dequantize + row gather, and MoEMLP (sorted gather_qmm)
-against the reference's per-expert loop restated with quantized_matmul
+QuantizedEmbedding == dequantize + row gather, FusedMLP against MLP, and
+MoEMLP (device routing, sorted gather_qmm, fused or split gate / up) against
+the reference's per-expert loop restated with quantized_matmul
 (mlx/src/nn/moe.rs:84-170)."""
 import pytest
 import torch
@@ -28,7 +29,21 @@ def test_quantized_linear_and_embedding():
     assert torch.equal(emb(tok), table[tok])
 
 
-def test_moe_matches_per_expert_loop():
+def test_fused_mlp_matches_mlp():
+    torch.manual_seed(2)
+    H, I = 512, 1536
+    dt = torch.bfloat16
+    lin = lambda o, i: nn.QuantizedLinear(*_q((torch.randn(o, i, device="cuda") * 0.02).to(dt)), 64, 4)
+    mlp = nn.MLP(lin(I, H), lin(I, H), lin(H, I))
+    fused = nn.FusedMLP.from_mlp(mlp)
+    for M in (1, 5, 200):
+        x = torch.randn(M, H, device="cuda").to(dt)
+        ref, got = mlp(x).float(), fused(x).float()
+        assert ((got - ref).abs().max() / ref.abs().max()).item() <= 1e-2
+
+
+@pytest.mark.parametrize("fused", [False, True])
+def test_moe_matches_per_expert_loop(fused):
     torch.manual_seed(1)
     E, H, I, k, T = 16, 256, 128, 4, 37
     dt = torch.bfloat16
@@ -45,7 +60,8 @@ def test_moe_matches_per_expert_loop():
                f"{p}.mlp.experts.down_proj.weight": down[0],
                f"{p}.mlp.experts.down_proj.scales": down[1],
                f"{p}.mlp.experts.down_proj.biases": down[2]}
-    experts = nn.split_fused_experts(weights, p, 64, 4)
+    experts = (nn.stack_fused_experts if fused else nn.split_fused_experts)(weights, p, 64, 4)
+    split = nn.split_fused_experts(weights, p, 64, 4)
     router = nn.Linear((torch.randn(E, H, device="cuda") * 0.1).to(dt))
     sh = [nn.QuantizedLinear(*_q((torch.randn(o, i, device="cuda") * 0.02).to(dt)), 64, 4)
           for (o, i) in [(I, H), (I, H), (H, I)]]
@@ -65,7 +81,7 @@ def test_moe_matches_per_expert_loop():
             continue
         xe = xf[rows]
         def proj(name, v):
-            st = experts[name]
+            st = split[name]
             return ops.quantized_matmul(v, st.weight[e], st.scales[e], st.biases[e], True, 64, 4)
         ye = proj("down", F.silu(proj("gate", xe)) * proj("up", xe))
         ref.index_add_(0, rows, ye.float() * scores[rows, slots].unsqueeze(-1))
