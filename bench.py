@@ -283,6 +283,133 @@ def bench_llama_decode(ops, Ms=(1, 4, 8, 16, 32), steps=5):
     return out
 
 
+def _graph_layers(fns, reps=5):
+    """Average device time of one pass over fns (captured once as a graph)."""
+    def step():
+        for f in fns:
+            f()
+    step()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    g.replay()
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(reps):
+        g.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    del g
+    return t0.elapsed_time(t1) * 1e-3 / reps
+
+
+def bench_fused(ops, Ms=(1, 4, 16), layers=32):
+    """The caller-side paths around the quantized ops, each against the
+    composition it replaces:
+    * Llama-3-8B MLP gate + up (4096 -> 2 x 14336, q4 gs64): two
+      quantized_matmul + silu * up (mlx/src/nn/mlp.rs:27-33) vs one fused
+      quantized_swiglu, over `layers` distinct weights (HIP-graph replay);
+    * Qwen3.5-MoE expert block (E=256, top-8, 2048 -> 2 x 512 -> 2048):
+      routing + sort + fused gate_up gather + down gather + combine, all on
+      the device, vs the same with torch softmax / topk / argsort / index_add
+      and split gate / up gathers;
+    * quantized embedding (vocab 128256 x 4096): row gather vs full-table
+      dequantize + index_select (mlx/src/nn/embedding.rs:62-72)."""
+    import torch.nn.functional as F
+    from ironmlx_amd import nn
+    gen = torch.Generator(device="cuda").manual_seed(6)
+    out = {}
+    H, I = 4096, 14336
+    gu = [make_weight(ops, 2 * I, H, gen) for _ in range(layers)]
+    wbytes = gu[0][0].numel() * 4 + gu[0][1].numel() * 4
+    mlp = {}
+    for M in Ms:
+        x = torch.randn((M, H), generator=gen, device="cuda").to(torch.bfloat16)
+        def unfused():
+            fs = []
+            for (wq, sq, bq) in gu:
+                def f(wq=wq, sq=sq, bq=bq):
+                    g = ops.quantized_matmul(x, wq[:I], sq[:I], bq[:I], True, 64, 4)
+                    u = ops.quantized_matmul(x, wq[I:], sq[I:], bq[I:], True, 64, 4)
+                    return F.silu(g) * u
+                fs.append(f)
+            return fs
+        fused = [lambda wq=wq, sq=sq, bq=bq: ops.quantized_swiglu(x, wq, sq, bq, 64, 4) for (wq, sq, bq) in gu]
+        tu = _graph_layers(unfused()) / layers
+        tf = _graph_layers(fused) / layers
+        mlp[str(M)] = {"unfused_us": round(tu * 1e6, 2), "fused_us": round(tf * 1e6, 2),
+                       "fused_weight_gbs": round(wbytes / tf / 1e9, 1)}
+    out["llama_gate_up_swiglu"] = mlp
+    del gu
+    torch.cuda.empty_cache()
+
+    E, Hm, Im, k = 256, 2048, 512, 8
+    def stack(n, kk):
+        w = torch.randint(-2**31, 2**31 - 1, (E, n, kk // 8), generator=gen, device="cuda",
+                          dtype=torch.int32).view(torch.uint32)
+        sc = (torch.rand((E, n, kk // 64), generator=gen, device="cuda") * 0.004 + 0.002).to(torch.bfloat16)
+        bi = (torch.randn((E, n, kk // 64), generator=gen, device="cuda") * 0.02).to(torch.bfloat16)
+        return w, sc, bi
+    gu_w, down_w = stack(2 * Im, Hm), stack(Hm, Im)
+    fused_ex = {"gate_up": nn.StackedExperts(*gu_w), "down": nn.StackedExperts(*down_w)}
+    split_ex = {"gate": nn.StackedExperts(gu_w[0][:, :Im].contiguous(), gu_w[1][:, :Im].contiguous(),
+                                          gu_w[2][:, :Im].contiguous()),
+                "up": nn.StackedExperts(gu_w[0][:, Im:].contiguous(), gu_w[1][:, Im:].contiguous(),
+                                        gu_w[2][:, Im:].contiguous()),
+                "down": nn.StackedExperts(*down_w)}
+    moe = {}
+    for T in (1, 64, 512):
+        logits = torch.randn((T, E), generator=gen, device="cuda").to(torch.bfloat16)
+        x = torch.randn((T, Hm), generator=gen, device="cuda").to(torch.bfloat16)
+        dev = nn.MoEMLP(None, fused_ex, None, None, k, True)
+
+        def on_device():
+            sc, ex = ops.moe_route(logits, k, True)
+            return dev.experts_forward(x, sc, ex)
+
+        def torch_routing():
+            p = torch.softmax(logits.float(), -1)
+            sc, ex = torch.topk(p, k, -1)
+            sc = sc / sc.sum(-1, keepdim=True)
+            flat = ex.reshape(-1)
+            order = torch.argsort(flat, stable=True)
+            rhs = flat[order].to(torch.int32)
+            xs = x[order // k].reshape(T * k, 1, Hm)
+            g = ops.gather_qmm(xs, split_ex["gate"].weight, split_ex["gate"].scales, split_ex["gate"].biases,
+                               None, rhs, True, 64, 4, "affine", True)
+            u = ops.gather_qmm(xs, split_ex["up"].weight, split_ex["up"].scales, split_ex["up"].biases,
+                               None, rhs, True, 64, 4, "affine", True)
+            h = (F.silu(g) * u).contiguous()
+            y = ops.gather_qmm(h, split_ex["down"].weight, split_ex["down"].scales, split_ex["down"].biases,
+                               None, rhs, True, 64, 4, "affine", True).reshape(T * k, -1)
+            o = torch.zeros((T, Hm), dtype=torch.float32, device="cuda")
+            o.index_add_(0, order // k, y.float() * sc.reshape(-1)[order].unsqueeze(-1))
+            return o
+
+        td = _graph_layers([on_device], reps=10)
+        tt = _graph_layers([torch_routing], reps=10)
+        moe[str(T)] = {"device_routing_fused_us": round(td * 1e6, 2), "torch_routing_split_us": round(tt * 1e6, 2)}
+    out["qwen_moe_expert_block"] = moe
+    del gu_w, down_w, fused_ex, split_ex
+    torch.cuda.empty_cache()
+
+    V, Hd = 128256, 4096
+    ew, es, eb = make_weight(ops, V, Hd, gen)
+    emb = {}
+    for T in (1, 512):
+        tok = torch.randint(0, V, (T,), generator=gen, device="cuda")
+        tg = _graph_layers([lambda: ops.dequantize_rows(ew, es, eb, tok, 64, 4)], reps=10)
+        tf = _graph_layers([lambda: ops.dequantize(ew, es, eb, 64, 4).index_select(0, tok)], reps=3)
+        emb[str(T)] = {"row_gather_us": round(tg * 1e6, 2), "full_table_dequant_us": round(tf * 1e6, 2)}
+    out["embedding_lookup_vocab128256_h4096"] = emb
+    del ew, es, eb
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(seconds=10.0, N=14336, K=4096):
     """The oracle's streaming GEMV (oracle/iqmm_oracle.c iqo_qmv_affine) on the
     host, same shape as the headline; bounded sample of ~`seconds`."""
@@ -324,6 +451,8 @@ def run_only(ops, args):
         return {"only": "moe", **bench_moe(ops)}
     if args.only == "sweep":
         return {"only": "sweep", **bench_mode_sweep(ops)}
+    if args.only == "fused":
+        return {"only": "fused", **bench_fused(ops)}
     nbytes = 256 << 20
     a = torch.empty(nbytes // 4, dtype=torch.int32, device="cuda").fill_(1)
     b = torch.empty_like(a)
@@ -352,7 +481,7 @@ def main():
     ap.add_argument("--no-llama", action="store_true")
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--only", choices=["gemv", "prefill", "moe", "sweep", "copy"], default=None,
+    ap.add_argument("--only", choices=["gemv", "prefill", "moe", "sweep", "fused", "copy"], default=None,
                     help="run one workload (for rocprofv3 kernel-trace / counter passes)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -374,6 +503,7 @@ def main():
     moe = bench_moe(ops)
     sweep = None if args.no_sweep else bench_mode_sweep(ops)
     llama = None if args.no_llama else bench_llama_decode(ops)
+    fused = bench_fused(ops)
     tr = load_traffic()
     traffic = tr.get("gemv_q4_gs64_k4096_n14336_m1", {}).get("traffic_bytes")
     traffic_pf = tr.get("prefill_q4_gs64_m2048_k4096_n14336", {}).get("traffic_bytes")
@@ -410,6 +540,7 @@ def main():
                                  "traffic": traffic_pf},
                     "down_proj_K14336_N4096_tflops": round(prefill_down["tflops"], 2)},
         "moe_gather_qmm": moe,
+        "fused_paths": fused,
     }
     if sweep is not None:
         line["mode_sweep_k4096_n4096"] = sweep

@@ -436,15 +436,19 @@ int gather_entry(const char* op, iqmm_array* res, iqmm_array x, iqmm_array w, iq
   // output batch one-to-one, so expert segments are contiguous in it
   const bool one_to_one = present(rhs) && numel(rhs) == a.nbatch &&
                           (present(lhs) ? numel(lhs) == a.nbatch : nxm == a.nbatch);
-  const bool grouped = sorted_indices && one_to_one && nwm + 1 <= 65535;
-  auto product = [&](QmmArgs& p) {
-    if (grouped && gather_sorted_supported(p)) return launch_gather_sorted(p, p.nbatch, nwm);
-    return run_qmm(p);
-  };
-  // few rows: the fused GEMV (one wave per output pair); many sorted rows:
-  // the grouped kernel, whose weight tiles serve every row of an expert
-  constexpr int64_t kFusedRows = 16;
-  hipError_t e = glu ? run_glu(a, !grouped || a.nbatch * a.M <= kFusedRows, product) : product(a);
+  // Sorted rows go to the grouped kernel (each expert's weights read once for
+  // all of its rows), except where the M = 1 GEMV applies and experts hold at
+  // most 4 rows on average: there the per-row GEMV, whose repeated weight
+  // reads hit the caches, was measured faster (T = 64 of a 256-expert top-8
+  // routing).  The fused SwiGLU follows the same choice.
+  const int64_t rows_per_expert = a.nbatch * a.M / (nwm > 0 ? nwm : 1);
+  QmmArgs probe = a;
+  probe.N = glu ? 2 * a.N : a.N;
+  const bool gemv_ok = qmv_q4_m1_supported(probe);
+  const bool grouped = sorted_indices && one_to_one && nwm + 1 <= 65535 && gather_sorted_supported(a) &&
+                       !(gemv_ok && rows_per_expert <= 4);
+  auto product = [&](QmmArgs& p) { return grouped ? launch_gather_sorted(p, p.nbatch, nwm) : run_qmm(p); };
+  hipError_t e = glu ? run_glu(a, !grouped, product) : product(a);
   return e == hipSuccess ? 0 : hip_fail(op, e);
 }
 }  // namespace
@@ -648,6 +652,7 @@ int iqmm_moe_combine(iqmm_array* res, iqmm_array y, iqmm_array inverse, iqmm_arr
   if (!present(experts) || experts.ndim != 2 || experts.dtype != IQMM_INT32)
     return fail("[%s] experts must be a 2D int32 array [tokens, k].", op);
   const int64_t T = experts.shape[0], k = experts.shape[1];
+  if (k > 32) return fail("[%s] at most 32 experts per token, got %lld.", op, (long long)k);
   if (!present(scores) || scores.dtype != IQMM_FLOAT32 || numel(scores) != T * k)
     return fail("[%s] scores must be float32 with the experts' %lld entries.", op, (long long)(T * k));
   if (!present(inverse) || inverse.dtype != IQMM_INT32 || numel(inverse) != T * k)

@@ -146,34 +146,60 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(const int32_t* experts, 
 }
 
 // out[t, d] = sum over t's valid slots in ascending sorted position (=
-// ascending expert) of float(y[pos, d]) * score
+// ascending expert) of float(y[pos, d]) * score.  One workgroup per token:
+// the k slots are ranked by position once (in LDS), then each thread runs the
+// ordered sum for its column (blockIdx.y picks 256 columns).
 template <int DT>
 __global__ __launch_bounds__(256) void moe_combine_kernel(const typename Store<DT>::T* y, const int32_t* inverse,
                                                           const int32_t* experts, const float* scores, float* out,
                                                           int T, int k, int64_t D, int E, int64_t n) {
-  const int64_t d = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (d >= D) return;
-  for (int t = blockIdx.y; t < T; t += gridDim.y) {
+  __shared__ int64_t rowoff[32];
+  __shared__ float wt[32];
+  __shared__ int nvalid;
+  const int tid = threadIdx.x;
+  for (int t = blockIdx.x; t < T; t += gridDim.x) {
     const int64_t base = static_cast<int64_t>(t) * k;
-    float acc = 0.f;
-    bool first = true;
-    int prev = -1;
-    for (int it = 0; it < k; ++it) {
-      // next slot: smallest sorted position above prev
-      int best = 0x7fffffff, bs = -1;
-      for (int sl = 0; sl < k; ++sl) {
-        const int pos = inverse[base + sl];
-        if (pos > prev && pos < best && pos < n) { best = pos; bs = sl; }  // rows outside y are skipped
+    if (tid == 0) nvalid = 0;
+    __syncthreads();
+    if (tid < k) {
+      const int pos = inverse[base + tid];
+      const int e = experts[base + tid];
+      const bool ok = pos >= 0 && pos < n && e >= 0 && e < E;
+      // rank among the valid slots by sorted position (slot order breaks ties,
+      // so ranks stay distinct even for repeated positions)
+      int rank = 0;
+      for (int j = 0; j < k; ++j) {
+        const int pj = inverse[base + j], ej = experts[base + j];
+        const bool okj = pj >= 0 && pj < n && ej >= 0 && ej < E;
+        rank += (okj && (pj < pos || (pj == pos && j < tid))) ? 1 : 0;
       }
-      if (bs < 0) break;
-      prev = best;
-      const int e = experts[base + bs];
-      if (e < 0 || e >= E) continue;
-      const float v = to_f<DT>(y[static_cast<int64_t>(best) * D + d]) * scores[base + bs];
-      acc = first ? v : acc + v;
-      first = false;
+      if (ok) {
+        rowoff[rank] = static_cast<int64_t>(pos) * D;
+        wt[rank] = scores[base + tid];
+        atomicAdd(&nvalid, 1);
+      }
     }
-    out[static_cast<int64_t>(t) * D + d] = acc;
+    __syncthreads();
+    const int nv = nvalid;
+    const int64_t d = static_cast<int64_t>(blockIdx.y) * 256 + tid;
+    if (d < D) {
+      float acc = 0.f;
+      for (int i0 = 0; i0 < nv; i0 += 8) {
+        // the loads of up to 8 rows are issued before the ordered adds
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = i0 + j < nv ? to_f<DT>(y[rowoff[i0 + j] + d]) : 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          if (i0 + j < nv) {
+            const float p = v[j] * wt[i0 + j];
+            acc = i0 + j == 0 ? p : acc + p;
+          }
+        }
+      }
+      out[static_cast<int64_t>(t) * D + d] = acc;
+    }
+    __syncthreads();
   }
 }
 
@@ -235,7 +261,8 @@ hipError_t launch_moe_combine(const void* y, int dt, const int32_t* inverse, con
                               const float* scores, float* out, int T, int k, int64_t D, int E, int64_t n,
                               hipStream_t st) {
   if (T == 0 || D == 0) return hipSuccess;
-  const dim3 grid(static_cast<unsigned>((D + 255) / 256), static_cast<unsigned>(T < 65535 ? T : 65535));
+  if ((D + 255) / 256 > 65535) return hipErrorInvalidConfiguration;
+  const dim3 grid(static_cast<unsigned>(T < 1048576 ? T : 1048576), static_cast<unsigned>((D + 255) / 256));
   switch (dt) {
     case F32:
       hipLaunchKernelGGL(moe_combine_kernel<F32>, grid, dim3(256), 0, st, static_cast<const float*>(y), inverse,

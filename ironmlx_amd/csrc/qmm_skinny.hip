@@ -495,64 +495,62 @@ hipError_t launch_qmm_skinny_fac(const QmmArgs& a) {
 // Grouped gather_qmm for sorted expert indices (mlx-c gather_qmm with
 // sorted_indices = true; the MoE layer of mlx/src/nn/moe.rs:84-170 over the
 // stacked [E, N, K/pack] expert tensors of mlx/src/model/qwen35.rs:653-775).
-// blockIdx.y = expert e.  The workgroup binary-searches the sorted flat rhs
-// index array for its row segment [lo, hi), so each expert's weight rows are
-// read once for all of the tokens routed to it (in 32-row m tiles).  Segment
-// row r is batch element b = lo + r / Mx, matrix row r % Mx, x matrix lhs[b].
-template <int XT, int MODE, int BITS, int S>
-__global__ __launch_bounds__(64 * S) void gather_sorted_kernel(QmmArgs a, int64_t nflat) {
+// A pre-pass turns the sorted flat rhs index array into segment offsets
+// off[e] = first row whose expert is >= e (off[E] = end of the valid rows), so
+// every workgroup finds its row segment with two loads.  blockIdx.y = expert
+// e; each wave owns 16 output columns over the whole K, so the expert's
+// weight rows are read once for all of the tokens routed to it (in 32-row m
+// tiles).  Segment row r is batch element b = lo + r / Mx, matrix row r % Mx,
+// x matrix lhs[b].  Rows whose expert index is outside [0, E) sort before
+// off[0] or from off[E] on and get NaN rows (blockIdx.y = E).
+__global__ __launch_bounds__(256) void segment_offsets_kernel(const void* rhs, int rhs_dt, int64_t nflat,
+                                                              int64_t E, int64_t* off) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i > nflat) return;
+  auto key = [&](int64_t j) {
+    const int64_t v = load_index(rhs, rhs_dt, j);
+    return v < 0 ? int64_t{-1} : v > E ? E : v;
+  };
+  const int64_t kp = i > 0 ? key(i - 1) : -1;
+  const int64_t kc = i < nflat ? key(i) : E + 1;
+  for (int64_t e = kp + 1; e <= min(kc, E); ++e) off[e] = i;
+}
+
+// Workgroup = S <= 8 waves over CS 16-column strips of one expert; wave w
+// takes chunk groups [w IT, (w + 1) IT) of K (a chunk group is 128 k: 4 lane
+// quarters x 32 codes) for all CS strips and issues every weight / scale load
+// before its first MFMA (CS x IT x 1 KiB of weights in flight per wave); each
+// x fragment (an L2-resident operand, loaded one group at a time) feeds the CS
+// strips' MFMAs.  The S partial tiles are summed through LDS.
+template <int XT, int MODE, int BITS, int IT, int CS>
+__global__ __launch_bounds__(512) void gather_sorted_kernel(QmmArgs a, int64_t nflat, const int64_t* off) {
   using XS = uint16_t;
   constexpr bool AFF = MODE == AFFINE;
-  constexpr int MT = 2;
-  __shared__ float red[S * 32 * 17];
-  __shared__ int64_t seg[2];
+  __shared__ float red[8][CS][16 * 17];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int S = blockDim.x >> 6;
   const int Mx = a.M, N = a.N, K = a.K;
-  const int n0 = blockIdx.x * 16;
+  const int n0 = blockIdx.x * 16 * CS;
   const int64_t e = blockIdx.y;
   if (e == a.bm.nw) {
-    // the extra block row: batch elements whose expert index is out of
-    // [0, E) get NaN rows (they belong to no expert segment)
-    int64_t lo = 0, hi = nflat;
-    while (lo < hi) {
-      const int64_t mid = (lo + hi) >> 1;
-      if (load_index(a.bm.rhs, a.bm.rhs_dt, mid) < 0) lo = mid + 1; else hi = mid;
-    }
-    const int64_t first_valid = lo;
-    hi = nflat;
-    while (lo < hi) {
-      const int64_t mid = (lo + hi) >> 1;
-      if (load_index(a.bm.rhs, a.bm.rhs_dt, mid) < e) lo = mid + 1; else hi = mid;
-    }
-    const int64_t end_valid = lo;
+    // offsets are clamped into [0, nflat]: indices that are not sorted as
+    // promised give wrong rows, never out-of-range accesses
+    const int64_t first_valid = min(max(off[0], int64_t{0}), nflat);
+    const int64_t end_valid = min(max(off[e], first_valid), nflat);
     XS* o = static_cast<XS*>(a.out);
     const int64_t nbad = first_valid + (nflat - end_valid);
-    for (int64_t i = t; i < nbad * Mx * 16; i += 64 * S) {
-      const int64_t rr = i / 16, n = i % 16;
+    constexpr int NC = 16 * CS;
+    for (int64_t i = t; i < nbad * Mx * NC; i += blockDim.x) {
+      const int64_t rr = i / NC, n = i % NC;
       const int64_t bi = rr / Mx, mrow = rr % Mx;
       const int64_t b = bi < first_valid ? bi : end_valid + (bi - first_valid);
       if (n0 + n < N) o[(b * Mx + mrow) * N + n0 + n] = from_f<XT>(__builtin_nanf(""));
     }
     return;
   }
-  if (t == 0) {
-    // lower_bound(e), lower_bound(e + 1) over the sorted flat rhs indices
-    int64_t lo = 0, hi = nflat;
-    while (lo < hi) {
-      const int64_t mid = (lo + hi) >> 1;
-      if (load_index(a.bm.rhs, a.bm.rhs_dt, mid) < e) lo = mid + 1; else hi = mid;
-    }
-    int64_t lo2 = lo, hi2 = nflat;
-    while (lo2 < hi2) {
-      const int64_t mid = (lo2 + hi2) >> 1;
-      if (load_index(a.bm.rhs, a.bm.rhs_dt, mid) <= e) lo2 = mid + 1; else hi2 = mid;
-    }
-    seg[0] = lo;
-    seg[1] = lo2;
-  }
-  __syncthreads();
-  const int64_t blo = seg[0], bhi = seg[1];
-  if (blo >= bhi) return;
+  const int64_t blo = min(max(off[e], int64_t{0}), nflat);
+  const int64_t bhi = min(max(off[e + 1], blo), nflat);
+  if (blo >= bhi) return;  // workgroup-uniform
   const int64_t rows_total = (bhi - blo) * Mx;
   XS* out = static_cast<XS*>(a.out);
   const XS* x = static_cast<const XS*>(a.x);
@@ -564,86 +562,104 @@ __global__ __launch_bounds__(64 * S) void gather_sorted_kernel(QmmArgs a, int64_
   const uint8_t* s8 = static_cast<const uint8_t*>(a.s) + e * a.s_mat;
   const int64_t wpr = static_cast<int64_t>(K) * BITS / 32;
   const int nl = lane & 15, q = lane >> 4;
-  const int row = min(n0 + nl, N - 1);
-  const uint32_t* wrow = w + static_cast<int64_t>(row) * wpr;
-  const int P = K >> 7;
-  const int pb = (P * wave) / S, pe = (P * (wave + 1)) / S;
+  const int p0 = wave * IT;
 
-  for (int64_t r0 = 0; r0 < rows_total; r0 += 32) {
-    // this lane's x rows (A operand) for the two 16-row tiles
-    const XS* xrows[MT];
-    bool xv[MT];
+  // weights and scales of this wave's chunks for every strip: loaded once,
+  // reused by every m tile
+  uint32_t wd[CS][IT][BITS];
+  float sv[CS][IT], bv[CS][IT], s2[CS][IT];
 #pragma unroll
-    for (int i = 0; i < MT; ++i) {
-      const int64_t r = r0 + 16 * i + nl;
-      xv[i] = r < rows_total;
-      const int64_t b = blo + (xv[i] ? r : 0) / Mx;
-      const int64_t mrow = (xv[i] ? r : 0) % Mx;
-      const int64_t xm = a.bm.lhs ? load_index(a.bm.lhs, a.bm.lhs_dt, b) : b;
-      const bool inb = xm >= 0 && xm < a.bm.nx;
-      xv[i] = xv[i] && inb;
-      xrows[i] = x + (inb ? xm : 0) * a.x_mat + mrow * K;
-    }
-    f32x4_t acc[MT];
+  for (int cs = 0; cs < CS; ++cs) {
+    const int row = min(n0 + 16 * cs + nl, N - 1);
+    const uint32_t* wrow = w + static_cast<int64_t>(row) * wpr;
 #pragma unroll
-    for (int i = 0; i < MT; ++i) acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    for (int p = pb; p < pe; ++p) {
-      const int c = 4 * p + q;
-      uint32_t wd[BITS];
-      load_chunk<BITS>(wd, wrow + c * BITS);
+    for (int it = 0; it < IT; ++it) {
+      const int c = 4 * (p0 + it) + q;
+      load_chunk<BITS>(wd[cs][it], wrow + c * BITS);
       const int gi = (c * 32) / gs;
-      float sv, bv = 0.f, s2;
       if constexpr (AFF) {
-        sv = to_f<XT>(sp[static_cast<int64_t>(row) * G + gi]);
-        bv = to_f<XT>(bp[static_cast<int64_t>(row) * G + gi]);
-        s2 = sv;
+        sv[cs][it] = to_f<XT>(sp[static_cast<int64_t>(row) * G + gi]);
+        bv[cs][it] = to_f<XT>(bp[static_cast<int64_t>(row) * G + gi]);
+        s2[cs][it] = sv[cs][it];
       } else {
-        sv = fp_scale<MODE>(s8[static_cast<int64_t>(row) * G + gi]);
-        s2 = MODE == NVFP4 ? fp_scale<MODE>(s8[static_cast<int64_t>(row) * G + gi + 1]) : sv;
-      }
-      g_u32x4_t xa[MT][4];
-#pragma unroll
-      for (int i = 0; i < MT; ++i) {
-        const g_u32x4_t* xp = reinterpret_cast<const g_u32x4_t*>(xrows[i] + c * 32);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) xa[i][j] = xv[i] ? xp[j] : g_u32x4_t{0, 0, 0, 0};
-      }
-      uint32_t o[16];
-      if constexpr (AFF && BITS == 4)
-        deq4_fast<XT>(g_u32x4_t{wd[0], wd[1], wd[2], wd[3]}, sv, bv, o);
-      else
-        dequant32<XT, MODE, BITS>(wd, sv, bv, s2, o);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const g_u32x4_t wb4 = {o[4 * j], o[4 * j + 1], o[4 * j + 2], o[4 * j + 3]};
-#pragma unroll
-        for (int i = 0; i < MT; ++i) acc[i] = mfma16x<XT>(xa[i][j], wb4, acc[i]);
+        sv[cs][it] = fp_scale<MODE>(s8[static_cast<int64_t>(row) * G + gi]);
+        s2[cs][it] = MODE == NVFP4 ? fp_scale<MODE>(s8[static_cast<int64_t>(row) * G + gi + 1]) : sv[cs][it];
+        bv[cs][it] = 0.f;
       }
     }
+  }
+
+  for (int64_t r0 = 0; r0 < rows_total; r0 += 16) {
+    // this lane's x row (A operand) of the 16-row tile
+    const int64_t r = r0 + nl;
+    bool xv = r < rows_total;
+    const int64_t b = blo + (xv ? r : 0) / Mx;
+    const int64_t mrow = (xv ? r : 0) % Mx;
+    const int64_t xm = a.bm.lhs ? load_index(a.bm.lhs, a.bm.lhs_dt, b) : b;
+    const bool inb = xm >= 0 && xm < a.bm.nx;
+    xv = xv && inb;
+    const XS* xrow = x + (inb ? xm : 0) * a.x_mat + mrow * K;
+    f32x4_t acc[CS];
 #pragma unroll
-    for (int i = 0; i < MT; ++i)
+    for (int cs = 0; cs < CS; ++cs) acc[cs] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) red[(wave * 32 + 16 * i + 4 * q + rr) * 17 + nl] = acc[i][rr];
+    for (int it = 0; it < IT; ++it) {
+      g_u32x4_t xa[4];
+      const g_u32x4_t* xp = reinterpret_cast<const g_u32x4_t*>(xrow + (4 * (p0 + it) + q) * 32);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) xa[j] = xv ? xp[j] : g_u32x4_t{0, 0, 0, 0};
+#pragma unroll
+      for (int cs = 0; cs < CS; ++cs) {
+        uint32_t o[16];
+        if constexpr (AFF && BITS == 4)
+          deq4_fast<XT>(g_u32x4_t{wd[cs][it][0], wd[cs][it][1], wd[cs][it][2], wd[cs][it][3]}, sv[cs][it],
+                        bv[cs][it], o);
+        else
+          dequant32<XT, MODE, BITS>(wd[cs][it], sv[cs][it], bv[cs][it], s2[cs][it], o);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[cs] = mfma16x<XT>(xa[j], g_u32x4_t{o[4 * j], o[4 * j + 1], o[4 * j + 2], o[4 * j + 3]}, acc[cs]);
+      }
+    }
+    // D[m][n]: m = 4 q + rr, n = nl
+#pragma unroll
+    for (int cs = 0; cs < CS; ++cs)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) red[wave][cs][(4 * q + rr) * 17 + nl] = acc[cs][rr];
     __syncthreads();
-    for (int i = t; i < 32 * 16; i += 64 * S) {
-      const int m = i / 16, n = i % 16;
-      const int64_t r = r0 + m;
-      if (r < rows_total && n0 + n < N) {
+    for (int i = t; i < CS * 16 * 16; i += blockDim.x) {
+      const int cs = i / 256, m = (i / 16) % 16, n = i % 16;
+      const int64_t rm = r0 + m;
+      const int col = n0 + 16 * cs + n;
+      if (rm < rows_total && col < N) {
         float v = 0.f;
-#pragma unroll
-        for (int w2 = 0; w2 < S; ++w2) v += red[(w2 * 32 + m) * 17 + n];
-        const int64_t b = blo + r / Mx, mrow = r % Mx;
-        const int64_t xm = a.bm.lhs ? load_index(a.bm.lhs, a.bm.lhs_dt, b) : b;
-        const bool inb = xm >= 0 && xm < a.bm.nx;
-        out[(b * Mx + mrow) * N + n0 + n] = from_f<XT>(inb ? v : __builtin_nanf(""));
+        for (int w2 = 0; w2 < S; ++w2) v += red[w2][cs][m * 17 + n];
+        const int64_t bb = blo + rm / Mx, mr = rm % Mx;
+        const int64_t xi = a.bm.lhs ? load_index(a.bm.lhs, a.bm.lhs_dt, bb) : bb;
+        const bool ok = xi >= 0 && xi < a.bm.nx;
+        out[(bb * Mx + mr) * N + col] = from_f<XT>(ok ? v : __builtin_nanf(""));
       }
     }
     __syncthreads();
   }
 }
 
+// chunk groups per wave of the grouped gather (P = K / 128 groups): the
+// smallest of 1 / 2 / 4 (<= itmax) that splits K over at most 4 waves
+// (measured best: K = 512 -> 1 group x 4 waves, K = 2048 -> 4 x 4), else the
+// largest that keeps the workgroup at <= 8 waves; 0 if none fits
+int gather_groups_per_wave(int K, int itmax) {
+  const int P = K >> 7;
+  for (int it = 1; it <= itmax; it <<= 1)
+    if (P % it == 0 && P / it <= 4) return it;
+  for (int it = itmax; it >= 1; it >>= 1)
+    if (P % it == 0 && P / it <= 8) return it;
+  return 0;
+}
+
 bool gather_sorted_supported(const QmmArgs& a) {
-  return a.transpose && (a.xdt == BF16 || a.xdt == F16) && a.K % 128 == 0 && a.bm.rhs != nullptr;
+  return a.transpose && (a.xdt == BF16 || a.xdt == F16) && a.K % 128 == 0 && a.K >= 128 &&
+         gather_groups_per_wave(a.K, 4) > 0 && a.bm.rhs != nullptr;
 }
 
 bool qmm_skinny_supported(const QmmArgs& a) {
@@ -739,47 +755,77 @@ hipError_t skinny_by_mode(const QmmArgs& a) {
 }  // namespace
 
 namespace {
-template <int XT, int MODE, int BITS>
-hipError_t gather_launch_t(const QmmArgs& a, int64_t nflat, int64_t E) {
-  const int64_t ntiles = (a.N + 15) / 16;
-  if (ntiles <= 0 || E <= 0 || nflat <= 0) return hipSuccess;
-  if (E + 1 > 65535 || ntiles > 0x7fffffffLL) return hipErrorInvalidConfiguration;
-  const int P = a.K >> 7;
-  const int S = P >= 8 ? 4 : P >= 4 ? 2 : 1;
+template <int XT, int MODE, int BITS, int CS>
+hipError_t gather_launch_cs(const QmmArgs& a, int64_t nflat, int64_t E, const int64_t* off) {
+  const int64_t ntiles = (a.N + 16 * CS - 1) / (16 * CS);
+  if (ntiles > 0x7fffffffLL) return hipErrorInvalidConfiguration;
   const dim3 grid(static_cast<unsigned>(ntiles), static_cast<unsigned>(E + 1));
-  switch (S) {
-    case 4: hipLaunchKernelGGL((gather_sorted_kernel<XT, MODE, BITS, 4>), grid, dim3(256), 0, a.stream, a, nflat); break;
-    case 2: hipLaunchKernelGGL((gather_sorted_kernel<XT, MODE, BITS, 2>), grid, dim3(128), 0, a.stream, a, nflat); break;
-    default: hipLaunchKernelGGL((gather_sorted_kernel<XT, MODE, BITS, 1>), grid, dim3(64), 0, a.stream, a, nflat); break;
+  // IT chunk groups (128 k each, P = K / 128) per wave, P / IT <= 8 waves.
+  // Register budget with CS strips held at once: 4-bit affine (fast byte
+  // dequant) holds 4 groups, other widths 2, 8-bit codes 1 (CS = 1: 4 for all)
+  constexpr int ITMAX = CS == 1 ? 4 : MODE == AFFINE && BITS == 4 ? 4 : BITS == 8 ? 1 : 2;
+  const int it = gather_groups_per_wave(a.K, ITMAX);
+  const dim3 block(static_cast<unsigned>(64 * ((a.K >> 7) / it)));
+  switch (it) {
+    case 4:
+      if constexpr (ITMAX >= 4)
+        hipLaunchKernelGGL((gather_sorted_kernel<XT, MODE, BITS, 4, CS>), grid, block, 0, a.stream, a, nflat, off);
+      break;
+    case 2:
+      if constexpr (ITMAX >= 2)
+        hipLaunchKernelGGL((gather_sorted_kernel<XT, MODE, BITS, 2, CS>), grid, block, 0, a.stream, a, nflat, off);
+      break;
+    case 1: hipLaunchKernelGGL((gather_sorted_kernel<XT, MODE, BITS, 1, CS>), grid, block, 0, a.stream, a, nflat, off); break;
+    default: return hipErrorInvalidConfiguration;
   }
   return hipGetLastError();
 }
 
+template <int XT, int MODE, int BITS>
+hipError_t gather_launch_t(const QmmArgs& a, int64_t nflat, int64_t E, const int64_t* off) {
+  // four strips per wave: 4x the weight bytes in flight per wave and each x
+  // fragment shared by four MFMAs (measured faster than one strip at 2 and
+  // 16 rows per expert for both MoE projections)
+  return gather_launch_cs<XT, MODE, BITS, 4>(a, nflat, E, off);
+}
+
 template <int XT>
-hipError_t gather_by_mode(const QmmArgs& a, int64_t nflat, int64_t E) {
+hipError_t gather_by_mode(const QmmArgs& a, int64_t nflat, int64_t E, const int64_t* off) {
   switch (a.mode) {
     case AFFINE:
       switch (a.bits) {
-        case 2: return gather_launch_t<XT, AFFINE, 2>(a, nflat, E);
-        case 3: return gather_launch_t<XT, AFFINE, 3>(a, nflat, E);
-        case 4: return gather_launch_t<XT, AFFINE, 4>(a, nflat, E);
-        case 5: return gather_launch_t<XT, AFFINE, 5>(a, nflat, E);
-        case 6: return gather_launch_t<XT, AFFINE, 6>(a, nflat, E);
-        case 8: return gather_launch_t<XT, AFFINE, 8>(a, nflat, E);
+        case 2: return gather_launch_t<XT, AFFINE, 2>(a, nflat, E, off);
+        case 3: return gather_launch_t<XT, AFFINE, 3>(a, nflat, E, off);
+        case 4: return gather_launch_t<XT, AFFINE, 4>(a, nflat, E, off);
+        case 5: return gather_launch_t<XT, AFFINE, 5>(a, nflat, E, off);
+        case 6: return gather_launch_t<XT, AFFINE, 6>(a, nflat, E, off);
+        case 8: return gather_launch_t<XT, AFFINE, 8>(a, nflat, E, off);
       }
       break;
-    case MXFP4: return gather_launch_t<XT, MXFP4, 4>(a, nflat, E);
-    case MXFP8: return gather_launch_t<XT, MXFP8, 8>(a, nflat, E);
-    case NVFP4: return gather_launch_t<XT, NVFP4, 4>(a, nflat, E);
+    case MXFP4: return gather_launch_t<XT, MXFP4, 4>(a, nflat, E, off);
+    case MXFP8: return gather_launch_t<XT, MXFP8, 8>(a, nflat, E, off);
+    case NVFP4: return gather_launch_t<XT, NVFP4, 4>(a, nflat, E, off);
   }
   return hipErrorInvalidValue;
 }
 }  // namespace
 
 hipError_t launch_gather_sorted(const QmmArgs& a, int64_t nflat, int64_t E) {
-  if (a.xdt == BF16) return gather_by_mode<BF16>(a, nflat, E);
-  if (a.xdt == F16) return gather_by_mode<F16>(a, nflat, E);
-  return hipErrorInvalidValue;
+  if (a.xdt != BF16 && a.xdt != F16) return hipErrorInvalidValue;
+  if (a.N <= 0 || E <= 0 || nflat <= 0) return hipSuccess;
+  if (E + 1 > 65535) return hipErrorInvalidConfiguration;
+  // segment offsets in a stream-ordered workspace (capturable in a HIP graph)
+  int64_t* off = nullptr;
+  hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&off), static_cast<size_t>(E + 1) * sizeof(int64_t),
+                                a.stream);
+  if (e != hipSuccess) return e;
+  const int64_t nb = (nflat + 1 + 255) / 256;
+  hipLaunchKernelGGL(segment_offsets_kernel, dim3(static_cast<unsigned>(nb)), dim3(256), 0, a.stream, a.bm.rhs,
+                     a.bm.rhs_dt, nflat, E, off);
+  e = hipGetLastError();
+  if (e == hipSuccess) e = a.xdt == BF16 ? gather_by_mode<BF16>(a, nflat, E, off) : gather_by_mode<F16>(a, nflat, E, off);
+  const hipError_t f = hipFreeAsync(off, a.stream);
+  return e != hipSuccess ? e : f;
 }
 
 hipError_t launch_qmm_skinny(const QmmArgs& a) {

@@ -101,9 +101,8 @@ def test_gather_qmm_swiglu(ops, dt, T, sorted_):
         rhs = flat.contiguous().cuda()
         lhs = (torch.arange(T * k) // k).to(torch.int32).cuda()
     got = ops.gather_qmm_swiglu(x, w, s, b, lhs, rhs, sorted_indices=sorted_)
-    # up to 16 rows the fused call takes the per-row GEMV (the unsorted
-    # kernel family) even for sorted indices; beyond, the grouped kernel
-    gu = ops.gather_qmm(x, w, s, b, lhs, rhs, True, sorted_indices=sorted_ and T * k > 16)
+    # the fused call picks the same kernel family as gather_qmm for these rows
+    gu = ops.gather_qmm(x, w, s, b, lhs, rhs, True, sorted_indices=sorted_)
     torch.cuda.synchronize()
     assert got.shape == (T * k, 1, I)
     ref = oracle.swiglu(to_np(gu, dt).reshape(T * k, 2 * I), dt)
