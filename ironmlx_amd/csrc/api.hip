@@ -208,14 +208,17 @@ hipError_t run_qmm(QmmArgs& a) {
 int elt_size(int dt) { return dt == IQMM_FLOAT32 ? 4 : 2; }
 
 // Fused SwiGLU over a gate_up weight of 2I rows (a.N = I outputs): the M = 1
-// GEMV reduces each gate row and its up row in one wave and applies the
-// SwiGLU in its epilogue; every other shape computes the [.., M, 2I] product
+// GEMV reduces each gate row and its up row in one wave, and the factored
+// decode kernel (M <= 32) pairs a gate tile with its up tile in one
+// workgroup; both apply the SwiGLU in their epilogue.  Every other shape
+// computes the [.., M, 2I] product
 // into a stream-ordered workspace with the regular kernels (`product`) and
 // then runs the elementwise SwiGLU over it.
 template <class F>
 hipError_t run_glu(QmmArgs& a, bool try_fused, F&& product) {
   a.glu = 1;
   if (try_fused && qmv_q4_m1_supported(a)) return launch_qmv_q4_m1(a);
+  if (try_fused && a.nbatch <= 65535 && qmm_skinny_fac_supported(a)) return launch_qmm_skinny_fac(a);
   a.glu = 0;
   const int64_t I = a.N, rows = a.nbatch * a.M;
   void* out = a.out;

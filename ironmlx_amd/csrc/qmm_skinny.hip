@@ -283,8 +283,13 @@ __global__ __launch_bounds__(64 * S) void qmm_skinny16_kernel(QmmArgs a, int nmt
 // an all-ones B.  A wave covers NT 16-row weight tiles (x pairs and X are
 // shared by them) for the blocks [pb, pe) of K; the S waves of a workgroup
 // split K and their partial sums meet in LDS.
-template <int XT, int NT, int MT, int GB, int S, int NB = 2>
+// GLU (NT = 2): the weight holds 2N rows (gate [0, N), up [N, 2N)); the two
+// tiles of a workgroup are gate rows n0.. and the matching up rows, and the
+// epilogue writes silu(gate) * up for 16 output columns.
+template <int XT, int NT, int MT, int GB, int S, int NB = 2, bool GLU = false>
 __global__ __launch_bounds__(64 * S) void qmm_skinny_fac_kernel(QmmArgs a) {
+  static_assert(!GLU || NT == 2, "GLU pairs one gate tile with one up tile");
+  constexpr int NC = GLU ? 16 : 16 * NT;  // output columns per workgroup
   using XS = uint16_t;
   constexpr int RPT = 16 / GB;
   constexpr float CM = XT == BF16 ? 128.f : 1024.f;
@@ -294,14 +299,14 @@ __global__ __launch_bounds__(64 * S) void qmm_skinny_fac_kernel(QmmArgs a) {
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int M = a.M, N = a.N, K = a.K;
-  const int n0 = blockIdx.x * 16 * NT;
+  const int n0 = blockIdx.x * NC;
   const int64_t bb = blockIdx.y;
   XS* out = static_cast<XS*>(a.out) + bb * static_cast<int64_t>(M) * N;
   int64_t xb = 0, wb = 0;
   if (a.bm.ndim != 0 || a.bm.lhs != nullptr || a.bm.rhs != nullptr) {
     if (!map_batch(a.bm, bb, xb, wb)) {
-      for (int i = t; i < M * 16 * NT; i += 64 * S) {
-        const int m = i / (16 * NT), n = n0 + i % (16 * NT);
+      for (int i = t; i < M * NC; i += 64 * S) {
+        const int m = i / NC, n = n0 + i % NC;
         if (n < N) out[static_cast<int64_t>(m) * N + n] = from_f<XT>(__builtin_nanf(""));
       }
       return;
@@ -329,7 +334,7 @@ __global__ __launch_bounds__(64 * S) void qmm_skinny_fac_kernel(QmmArgs a) {
   const char* br[NT];
 #pragma unroll
   for (int tt = 0; tt < NT; ++tt) {
-    const int64_t n = min(n0 + 16 * tt + r, N - 1);
+    const int64_t n = GLU ? static_cast<int64_t>(tt) * N + min(n0 + r, N - 1) : min(n0 + 16 * tt + r, N - 1);
     wr[tt] = w + n * wrow;
     sr[tt] = sp + n * srow;
     br[tt] = bp + n * srow;
@@ -428,6 +433,20 @@ __global__ __launch_bounds__(64 * S) void qmm_skinny_fac_kernel(QmmArgs a) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) red[((wave * NT + tt) * MT + i) * 256 + (4 * q + v) * 16 + r] = Y[tt][i][v];
   __syncthreads();
+  if constexpr (GLU) {
+    for (int idx = t; idx < M * 16; idx += 64 * S) {
+      const int m = idx / 16, nn = idx % 16, i = m / RPT, mr = m % RPT;
+      float acc[2] = {0.f, 0.f};
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int w2 = 0; w2 < S; ++w2)
+#pragma unroll
+          for (int g = 0; g < GB; ++g) acc[tt] += red[((w2 * NT + tt) * MT + i) * 256 + (mr + RPT * g) * 16 + nn];
+      if (n0 + nn < N) out[static_cast<int64_t>(m) * N + n0 + nn] = swiglu_out<XT>(acc[0], acc[1]);
+    }
+    return;
+  }
   for (int idx = t; idx < M * 16 * NT; idx += 64 * S) {
     const int m = idx / (16 * NT), nn = idx % (16 * NT);
     const int tt = nn >> 4, i = m / RPT, mr = m % RPT;
@@ -441,37 +460,38 @@ __global__ __launch_bounds__(64 * S) void qmm_skinny_fac_kernel(QmmArgs a) {
 }
 
 namespace {
-template <int XT, int NT, int MT, int GB>
+template <int XT, int NT, int MT, int GB, bool GLU>
 hipError_t fac_launch_s(const QmmArgs& a, dim3 grid, int S) {
   switch (S) {
-    case 8: hipLaunchKernelGGL((qmm_skinny_fac_kernel<XT, NT, MT, GB, 8>), grid, dim3(512), 0, a.stream, a); break;
-    case 4: hipLaunchKernelGGL((qmm_skinny_fac_kernel<XT, NT, MT, GB, 4>), grid, dim3(256), 0, a.stream, a); break;
-    case 2: hipLaunchKernelGGL((qmm_skinny_fac_kernel<XT, NT, MT, GB, 2>), grid, dim3(128), 0, a.stream, a); break;
-    default: hipLaunchKernelGGL((qmm_skinny_fac_kernel<XT, NT, MT, GB, 1>), grid, dim3(64), 0, a.stream, a); break;
+    case 8: hipLaunchKernelGGL((qmm_skinny_fac_kernel<XT, NT, MT, GB, 8, 2, GLU>), grid, dim3(512), 0, a.stream, a); break;
+    case 4: hipLaunchKernelGGL((qmm_skinny_fac_kernel<XT, NT, MT, GB, 4, 2, GLU>), grid, dim3(256), 0, a.stream, a); break;
+    case 2: hipLaunchKernelGGL((qmm_skinny_fac_kernel<XT, NT, MT, GB, 2, 2, GLU>), grid, dim3(128), 0, a.stream, a); break;
+    default: hipLaunchKernelGGL((qmm_skinny_fac_kernel<XT, NT, MT, GB, 1, 2, GLU>), grid, dim3(64), 0, a.stream, a); break;
   }
   return hipGetLastError();
 }
-template <int XT, int GB>
+template <int XT, int GB, bool GLU>
 hipError_t fac_launch_gb(const QmmArgs& a) {
   constexpr int RPT = 16 / GB;
   constexpr int NT = 2;
-  const int64_t nwg = (a.N + 16 * NT - 1) / (16 * NT);
+  constexpr int NC = GLU ? 16 : 16 * NT;  // output columns per workgroup
+  const int64_t nwg = (a.N + NC - 1) / NC;
   if (nwg <= 0 || a.nbatch <= 0) return hipSuccess;
   if (nwg > 0x7fffffffLL || a.nbatch > 65535) return hipErrorInvalidConfiguration;
   const int P = a.K >> 7;
   int S = 1;
   while (S < 8 && P / (2 * S) >= 2 && nwg * a.nbatch * S < 4096) S *= 2;
   const dim3 grid(static_cast<unsigned>(nwg), static_cast<unsigned>(a.nbatch));
-  if (a.M <= RPT) return fac_launch_s<XT, NT, 1, GB>(a, grid, S);
-  if (a.M <= 2 * RPT) return fac_launch_s<XT, NT, 2, GB>(a, grid, S);
-  return fac_launch_s<XT, NT, 4, GB>(a, grid, S);
+  if (a.M <= RPT) return fac_launch_s<XT, NT, 1, GB, GLU>(a, grid, S);
+  if (a.M <= 2 * RPT) return fac_launch_s<XT, NT, 2, GB, GLU>(a, grid, S);
+  return fac_launch_s<XT, NT, 4, GB, GLU>(a, grid, S);
 }
-template <int XT>
+template <int XT, bool GLU>
 hipError_t fac_launch(const QmmArgs& a) {
   switch (a.gs) {
-    case 32: return fac_launch_gb<XT, 4>(a);
-    case 64: return fac_launch_gb<XT, 2>(a);
-    default: return fac_launch_gb<XT, 1>(a);
+    case 32: return fac_launch_gb<XT, 4, GLU>(a);
+    case 64: return fac_launch_gb<XT, 2, GLU>(a);
+    default: return fac_launch_gb<XT, 1, GLU>(a);
   }
 }
 }  // namespace
@@ -483,12 +503,14 @@ bool qmm_skinny_fac_supported(const QmmArgs& a) {
   const int rpt = 16 / (128 / a.gs);   // x rows per m tile
   // with fewer than 2048 waves (8 per 32-row tile pair) the split-K skinny
   // kernel keeps more loads in flight
-  const int64_t waves = (a.N + 31) / 32 * 8 * a.nbatch;
+  // (GLU: 2N weight rows, 16 output columns per workgroup)
+  const int64_t waves = (a.N + 31) / 32 * 8 * a.nbatch * (a.glu ? 2 : 1);
   return a.M >= 1 && a.M <= 4 * rpt && a.M <= 32 && waves >= 2048;
 }
 
 hipError_t launch_qmm_skinny_fac(const QmmArgs& a) {
-  return a.xdt == BF16 ? fac_launch<BF16>(a) : fac_launch<F16>(a);
+  if (a.glu) return a.xdt == BF16 ? fac_launch<BF16, true>(a) : fac_launch<F16, true>(a);
+  return a.xdt == BF16 ? fac_launch<BF16, false>(a) : fac_launch<F16, false>(a);
 }
 
 // ---------------------------------------------------------------------------

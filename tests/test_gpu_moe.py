@@ -47,7 +47,8 @@ def _weights(rng, mode, rows, K, dt, lead=()):
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
 @pytest.mark.parametrize("mode", ["affine", "mxfp4", "nvfp4"])
 @pytest.mark.parametrize("M,I,K", [(1, 300, 1024), (1, 2048, 4096), (1, 14336, 4096), (1, 4096, 14336),
-                                   (3, 512, 1024), (16, 1000, 2048), (128, 1024, 1024)])
+                                   (3, 512, 1024), (16, 1000, 2048), (128, 1024, 1024),
+                                   (4, 14336, 4096), (16, 4096, 4096), (32, 4100, 2048), (8, 2048, 4096)])
 def test_quantized_swiglu(ops, dt, mode, M, I, K):
     print(f"swiglu {mode} {dt} M={M} I={I} K={K}", flush=True)
     rng = np.random.default_rng(M * 7 + I + K)
