@@ -243,41 +243,63 @@ def bench_mode_sweep(ops, K=4096, N=4096, Ms=(1, 256), n=20):
 
 def bench_llama_decode(ops, Ms=(1, 4, 8, 16, 32), steps=5):
     """Llama-3-8B-shaped decode step: 32 layers x {q,k,v,o,gate,up,down} of
-    distinct 4-bit gs64 weights; tokens/s = M / step time."""
-    shapes = [(4096, 4096), (1024, 4096), (1024, 4096), (4096, 4096), (14336, 4096),
-              (14336, 4096), (4096, 14336)]
+    distinct 4-bit gs64 weights; tokens/s = M / step time.  gate and up are
+    the two row halves of one stacked [2 x 14336, 4096] weight, so the same
+    bytes also run the fused-MLP step (q, k, v, o, quantized_swiglu(gate_up),
+    down: six calls per layer instead of seven plus silu * up)."""
+    shapes = [(4096, 4096), (1024, 4096), (1024, 4096), (4096, 4096), (2 * 14336, 4096), (4096, 14336)]
     gen = torch.Generator(device="cuda").manual_seed(2)
     layers = [[make_weight(ops, N, K, gen) for (N, K) in shapes] for _ in range(32)]
     wbytes = sum(w.numel() * 4 + s.numel() * 2 * 2 for L in layers for (w, s, b) in L)
+    I = 14336
     out = {}
     stream = torch.cuda.current_stream()
     for M in Ms:
         xs = {K: torch.randn((M, K), generator=gen, device="cuda").to(torch.bfloat16)
               for K in (4096, 14336)}
+        h = torch.randn((M, I), generator=gen, device="cuda").to(torch.bfloat16)
 
-        def step():
+        def step_unfused():
             for L in layers:
-                for (w, s, b), (N, K) in zip(L, shapes):
-                    ops.quantized_matmul(xs[K], w, s, b, True, 64, 4, "affine")
+                for (w, s, b) in L[:4]:
+                    ops.quantized_matmul(xs[4096], w, s, b, True, 64, 4, "affine")
+                w, s, b = L[4]
+                ops.quantized_matmul(xs[4096], w[:I], s[:I], b[:I], True, 64, 4, "affine")
+                ops.quantized_matmul(xs[4096], w[I:], s[I:], b[I:], True, 64, 4, "affine")
+                w, s, b = L[5]
+                ops.quantized_matmul(xs[14336], w, s, b, True, 64, 4, "affine")
 
-        step()
-        torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
+        def step_fused():
+            for L in layers:
+                for (w, s, b) in L[:4]:
+                    ops.quantized_matmul(xs[4096], w, s, b, True, 64, 4, "affine")
+                w, s, b = L[4]
+                ops.quantized_swiglu(xs[4096], w, s, b, 64, 4)
+                w, s, b = L[5]
+                ops.quantized_matmul(h, w, s, b, True, 64, 4, "affine")
+
+        row = {}
+        for name, step in (("", step_unfused), ("fused_mlp_", step_fused)):
             step()
-        g.replay()
-        torch.cuda.synchronize()
-        t0 = torch.cuda.Event(enable_timing=True)
-        t1 = torch.cuda.Event(enable_timing=True)
-        t0.record(stream)
-        for _ in range(steps):
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                step()
             g.replay()
-        t1.record(stream)
-        torch.cuda.synchronize()
-        dt = t0.elapsed_time(t1) * 1e-3 / steps
-        out[str(M)] = {"ms_per_step": dt * 1e3, "tokens_per_s": M / dt,
-                       "weight_gbs": wbytes / dt / 1e9}
-        del g
+            torch.cuda.synchronize()
+            t0 = torch.cuda.Event(enable_timing=True)
+            t1 = torch.cuda.Event(enable_timing=True)
+            t0.record(stream)
+            for _ in range(steps):
+                g.replay()
+            t1.record(stream)
+            torch.cuda.synchronize()
+            dt = t0.elapsed_time(t1) * 1e-3 / steps
+            row[name + "ms_per_step"] = dt * 1e3
+            row[name + "tokens_per_s"] = M / dt
+            row[name + "weight_gbs"] = wbytes / dt / 1e9
+            del g
+        out[str(M)] = row
     del layers
     torch.cuda.empty_cache()
     return out
@@ -453,6 +475,8 @@ def run_only(ops, args):
         return {"only": "sweep", **bench_mode_sweep(ops)}
     if args.only == "fused":
         return {"only": "fused", **bench_fused(ops)}
+    if args.only == "llama":
+        return {"only": "llama", **bench_llama_decode(ops)}
     nbytes = 256 << 20
     a = torch.empty(nbytes // 4, dtype=torch.int32, device="cuda").fill_(1)
     b = torch.empty_like(a)
@@ -481,7 +505,7 @@ def main():
     ap.add_argument("--no-llama", action="store_true")
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--only", choices=["gemv", "prefill", "moe", "sweep", "fused", "copy"], default=None,
+    ap.add_argument("--only", choices=["gemv", "prefill", "moe", "sweep", "fused", "llama", "copy"], default=None,
                     help="run one workload (for rocprofv3 kernel-trace / counter passes)")
     args = ap.parse_args()
     if args.gpus != 1:
