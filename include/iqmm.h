@@ -40,11 +40,12 @@
  * the inferred ones.  Inputs are never modified or freed.  Work is enqueued on
  * `stream` (a hipStream_t; NULL = the null stream) and is complete after the
  * stream is synchronised, as after mlx's `eval` (mlx/src/array.rs:111-113).
- * The library's only device allocation is the fp32 partial-sum workspace of a
- * split-K GEMM (few output tiles, M > 64), taken with hipMallocAsync and
- * released with hipFreeAsync on `stream`, so it is stream-ordered and may be
- * captured in a HIP graph.  Calls are re-entrant; calls on one stream execute
- * in order.
+ * The library's device allocations are workspaces taken with hipMallocAsync
+ * and released with hipFreeAsync on `stream` (stream-ordered, capturable in
+ * a HIP graph): the fp32 partial sums of a split-K GEMM (few output tiles,
+ * M > 64), the gate_up product of a fused SwiGLU outside its fused kernels,
+ * and the expert segment offsets of a sorted grouped gather_qmm.  Calls are
+ * re-entrant; calls on one stream execute in order.
  */
 #ifndef IQMM_H
 #define IQMM_H

@@ -88,3 +88,22 @@ def test_moe_matches_per_expert_loop(fused):
     ref = ref + (shared(xf).float() * torch.sigmoid(sgate(xf).float()))
     err = ((got.reshape(T, H) - ref).abs().max() / ref.abs().max()).item()
     assert err <= 2e-2, err
+
+
+def test_checkpoint_layer_runs(tmp_path):
+    """A quantized layer read from a safetensors checkpoint (loader.rs:13-44
+    key scheme) feeds the kernels unchanged."""
+    import numpy as np
+    import safetensors.numpy as sn
+    import oracle
+    from ironmlx_amd import loader
+    rng = np.random.default_rng(1)
+    w = (rng.standard_normal((512, 1024)) * 0.02).astype(np.float32)
+    wq, s, b = oracle.affine_quantize(w, "f32", 64, 4, "f16")
+    sn.save_file({"p.weight": wq, "p.scales": s, "p.biases": b}, str(tmp_path / "model.safetensors"))
+    weights = loader.load_model_weights(str(tmp_path))
+    lin = loader.quantized_layers(weights, nn.QuantizationConfig())["p"]
+    x = rng.standard_normal((3, 1024)).astype(np.float16)
+    got = lin(torch.from_numpy(x).cuda()).cpu().numpy().astype(np.float64)
+    ref = oracle.qmm(x, "f16", wq, s, b, "f16", True, 64, 4).astype(np.float64)
+    assert np.max(np.abs(got - ref)) / np.max(np.abs(ref)) <= 1e-2
