@@ -283,13 +283,13 @@ __global__ __launch_bounds__(64 * S) void qmm_skinny16_kernel(QmmArgs a, int nmt
 // an all-ones B.  A wave covers NT 16-row weight tiles (x pairs and X are
 // shared by them) for the blocks [pb, pe) of K; the S waves of a workgroup
 // split K and their partial sums meet in LDS.
-// GLU (NT = 2): the weight holds 2N rows (gate [0, N), up [N, 2N)); the two
-// tiles of a workgroup are gate rows n0.. and the matching up rows, and the
-// epilogue writes silu(gate) * up for 16 output columns.
+// GLU (NT even): the weight holds 2N rows (gate [0, N), up [N, 2N)); tiles
+// [0, NT/2) of a workgroup are gate rows n0.. and tiles [NT/2, NT) the
+// matching up rows, and the epilogue writes silu(gate) * up for 8 NT columns.
 template <int XT, int NT, int MT, int GB, int S, int NB = 2, bool GLU = false>
 __global__ __launch_bounds__(64 * S) void qmm_skinny_fac_kernel(QmmArgs a) {
-  static_assert(!GLU || NT == 2, "GLU pairs one gate tile with one up tile");
-  constexpr int NC = GLU ? 16 : 16 * NT;  // output columns per workgroup
+  static_assert(!GLU || NT % 2 == 0, "GLU pairs gate tiles with up tiles");
+  constexpr int NC = GLU ? 8 * NT : 16 * NT;  // output columns per workgroup
   using XS = uint16_t;
   constexpr int RPT = 16 / GB;
   constexpr float CM = XT == BF16 ? 128.f : 1024.f;
@@ -334,7 +334,8 @@ __global__ __launch_bounds__(64 * S) void qmm_skinny_fac_kernel(QmmArgs a) {
   const char* br[NT];
 #pragma unroll
   for (int tt = 0; tt < NT; ++tt) {
-    const int64_t n = GLU ? static_cast<int64_t>(tt) * N + min(n0 + r, N - 1) : min(n0 + 16 * tt + r, N - 1);
+    const int64_t n = GLU ? static_cast<int64_t>(tt / (NT / 2)) * N + min(n0 + 16 * (tt % (NT / 2)) + r, N - 1)
+                          : min(n0 + 16 * tt + r, N - 1);
     wr[tt] = w + n * wrow;
     sr[tt] = sp + n * srow;
     br[tt] = bp + n * srow;
@@ -434,15 +435,18 @@ __global__ __launch_bounds__(64 * S) void qmm_skinny_fac_kernel(QmmArgs a) {
       for (int v = 0; v < 4; ++v) red[((wave * NT + tt) * MT + i) * 256 + (4 * q + v) * 16 + r] = Y[tt][i][v];
   __syncthreads();
   if constexpr (GLU) {
-    for (int idx = t; idx < M * 16; idx += 64 * S) {
-      const int m = idx / 16, nn = idx % 16, i = m / RPT, mr = m % RPT;
+    for (int idx = t; idx < M * NC; idx += 64 * S) {
+      const int m = idx / NC, nn = idx % NC, i = m / RPT, mr = m % RPT;
+      const int sub = nn >> 4;
       float acc[2] = {0.f, 0.f};
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt)
+      for (int h = 0; h < 2; ++h) {
+        const int tt = h * (NT / 2) + sub;
 #pragma unroll
         for (int w2 = 0; w2 < S; ++w2)
 #pragma unroll
-          for (int g = 0; g < GB; ++g) acc[tt] += red[((w2 * NT + tt) * MT + i) * 256 + (mr + RPT * g) * 16 + nn];
+          for (int g = 0; g < GB; ++g) acc[h] += red[((w2 * NT + tt) * MT + i) * 256 + (mr + RPT * g) * 16 + (nn & 15)];
+      }
       if (n0 + nn < N) out[static_cast<int64_t>(m) * N + n0 + nn] = swiglu_out<XT>(acc[0], acc[1]);
     }
     return;
@@ -460,31 +464,44 @@ __global__ __launch_bounds__(64 * S) void qmm_skinny_fac_kernel(QmmArgs a) {
 }
 
 namespace {
-template <int XT, int NT, int MT, int GB, bool GLU>
-hipError_t fac_launch_s(const QmmArgs& a, dim3 grid, int S) {
+template <int XT, int NT, int MT, int GB, bool GLU, int NB>
+hipError_t fac_launch_nb(const QmmArgs& a, dim3 grid, int S) {
   switch (S) {
-    case 8: hipLaunchKernelGGL((qmm_skinny_fac_kernel<XT, NT, MT, GB, 8, 2, GLU>), grid, dim3(512), 0, a.stream, a); break;
-    case 4: hipLaunchKernelGGL((qmm_skinny_fac_kernel<XT, NT, MT, GB, 4, 2, GLU>), grid, dim3(256), 0, a.stream, a); break;
-    case 2: hipLaunchKernelGGL((qmm_skinny_fac_kernel<XT, NT, MT, GB, 2, 2, GLU>), grid, dim3(128), 0, a.stream, a); break;
-    default: hipLaunchKernelGGL((qmm_skinny_fac_kernel<XT, NT, MT, GB, 1, 2, GLU>), grid, dim3(64), 0, a.stream, a); break;
+    case 8: hipLaunchKernelGGL((qmm_skinny_fac_kernel<XT, NT, MT, GB, 8, NB, GLU>), grid, dim3(512), 0, a.stream, a); break;
+    case 4: hipLaunchKernelGGL((qmm_skinny_fac_kernel<XT, NT, MT, GB, 4, NB, GLU>), grid, dim3(256), 0, a.stream, a); break;
+    case 2: hipLaunchKernelGGL((qmm_skinny_fac_kernel<XT, NT, MT, GB, 2, NB, GLU>), grid, dim3(128), 0, a.stream, a); break;
+    default: hipLaunchKernelGGL((qmm_skinny_fac_kernel<XT, NT, MT, GB, 1, NB, GLU>), grid, dim3(64), 0, a.stream, a); break;
   }
   return hipGetLastError();
 }
-template <int XT, int GB, bool GLU>
-hipError_t fac_launch_gb(const QmmArgs& a) {
-  constexpr int RPT = 16 / GB;
-  constexpr int NT = 2;
-  constexpr int NC = GLU ? 16 : 16 * NT;  // output columns per workgroup
+template <int XT, int NT, int MT, int GB, bool GLU>
+hipError_t fac_launch_s(const QmmArgs& a, dim3 grid, int S) {
+  return fac_launch_nb<XT, NT, MT, GB, GLU, 2>(a, grid, S);
+}
+template <int XT, int GB, bool GLU, int NT, int MT>
+hipError_t fac_launch_gbn(const QmmArgs& a) {
+  constexpr int NC = GLU ? 8 * NT : 16 * NT;  // output columns per workgroup
   const int64_t nwg = (a.N + NC - 1) / NC;
   if (nwg <= 0 || a.nbatch <= 0) return hipSuccess;
   if (nwg > 0x7fffffffLL || a.nbatch > 65535) return hipErrorInvalidConfiguration;
   const int P = a.K >> 7;
   int S = 1;
   while (S < 8 && P / (2 * S) >= 2 && nwg * a.nbatch * S < 4096) S *= 2;
+  // the LDS partial tiles (S NT MT KiB) stay within 64 KiB so two workgroups fit a CU
+  while (S > 1 && S * NT * MT > 64) S >>= 1;
   const dim3 grid(static_cast<unsigned>(nwg), static_cast<unsigned>(a.nbatch));
-  if (a.M <= RPT) return fac_launch_s<XT, NT, 1, GB, GLU>(a, grid, S);
-  if (a.M <= 2 * RPT) return fac_launch_s<XT, NT, 2, GB, GLU>(a, grid, S);
-  return fac_launch_s<XT, NT, 4, GB, GLU>(a, grid, S);
+  return fac_launch_s<XT, NT, MT, GB, GLU>(a, grid, S);
+}
+template <int XT, int GB, bool GLU>
+hipError_t fac_launch_gb(const QmmArgs& a) {
+  // With two or more m tiles the x fragments (loaded per wave from L2) cost
+  // more than the weights; four weight tiles per wave halve the x loads per
+  // weight byte (measured 24.2 -> 21.4 us at M = 16, 35.6 -> 32.6 us at M = 32,
+  // N = 14336, K = 4096); with GLU, two gate and two up tiles.
+  constexpr int RPT = 16 / GB;
+  if (a.M <= RPT) return fac_launch_gbn<XT, GB, GLU, 2, 1>(a);
+  if (a.M <= 2 * RPT) return fac_launch_gbn<XT, GB, GLU, 4, 2>(a);
+  return fac_launch_gbn<XT, GB, GLU, 4, 4>(a);
 }
 template <int XT, bool GLU>
 hipError_t fac_launch(const QmmArgs& a) {
