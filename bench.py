@@ -246,12 +246,15 @@ def bench_llama_decode(ops, Ms=(1, 4, 8, 16, 32), steps=5):
     distinct 4-bit gs64 weights; tokens/s = M / step time.  gate and up are
     the two row halves of one stacked [2 x 14336, 4096] weight, so the same
     bytes also run the fused-MLP step (q, k, v, o, quantized_swiglu(gate_up),
-    down: six calls per layer instead of seven plus silu * up)."""
+    down: six calls per layer instead of seven plus silu * up), and with q, k,
+    v stacked into one weight the fused-QKV-and-MLP step (four calls)."""
     shapes = [(4096, 4096), (1024, 4096), (1024, 4096), (4096, 4096), (2 * 14336, 4096), (4096, 14336)]
     gen = torch.Generator(device="cuda").manual_seed(2)
     layers = [[make_weight(ops, N, K, gen) for (N, K) in shapes] for _ in range(32)]
     wbytes = sum(w.numel() * 4 + s.numel() * 2 * 2 for L in layers for (w, s, b) in L)
     I = 14336
+    # the fused-QKV variant reads the same bytes from one stacked weight per layer
+    qkv = [tuple(torch.cat([L[i][j] for i in range(3)], dim=0) for j in range(3)) for L in layers]
     out = {}
     stream = torch.cuda.current_stream()
     for M in Ms:
@@ -278,8 +281,20 @@ def bench_llama_decode(ops, Ms=(1, 4, 8, 16, 32), steps=5):
                 w, s, b = L[5]
                 ops.quantized_matmul(h, w, s, b, True, 64, 4, "affine")
 
+        def step_fused_qkv():
+            # q, k, v stacked row-wise (one [6144, 4096] weight per layer: the
+            # first three weights of a layer are contiguous row blocks of it)
+            for L, QKV in zip(layers, qkv):
+                ops.quantized_matmul(xs[4096], *QKV, True, 64, 4, "affine")
+                w, s, b = L[3]
+                ops.quantized_matmul(xs[4096], w, s, b, True, 64, 4, "affine")
+                w, s, b = L[4]
+                ops.quantized_swiglu(xs[4096], w, s, b, 64, 4)
+                w, s, b = L[5]
+                ops.quantized_matmul(h, w, s, b, True, 64, 4, "affine")
+
         row = {}
-        for name, step in (("", step_unfused), ("fused_mlp_", step_fused)):
+        for name, step in (("", step_unfused), ("fused_mlp_", step_fused), ("fused_qkv_mlp_", step_fused_qkv)):
             step()
             torch.cuda.synchronize()
             g = torch.cuda.CUDAGraph()
@@ -300,7 +315,7 @@ def bench_llama_decode(ops, Ms=(1, 4, 8, 16, 32), steps=5):
             row[name + "weight_gbs"] = wbytes / dt / 1e9
             del g
         out[str(M)] = row
-    del layers
+    del layers, qkv
     torch.cuda.empty_cache()
     return out
 

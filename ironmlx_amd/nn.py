@@ -170,6 +170,25 @@ class FusedMLP:
         return self.down_proj(h, stream)
 
 
+class FusedQKV:
+    """q, k and v projections of one attention layer stacked row-wise into a
+    single QuantizedLinear ([Nq + Nk + Nv, K/pack]) so decode reads x once and
+    runs one GEMV instead of three; returns the (q, k, v) column blocks.
+    Each block equals its own projection's output (the rows are independent)."""
+
+    def __init__(self, q: QuantizedLinear, k: QuantizedLinear, v: QuantizedLinear):
+        params = {(p.group_size, p.bits, p.mode) for p in (q, k, v)}
+        if len(params) != 1:
+            raise ValueError("q, k and v must share group_size, bits and mode")
+        cat = lambda *t: None if t[0] is None else torch.cat(t, dim=0).contiguous()
+        self.linear = QuantizedLinear(cat(q.weight, k.weight, v.weight), cat(q.scales, k.scales, v.scales),
+                                      cat(q.biases, k.biases, v.biases), q.group_size, q.bits, q.mode)
+        self.sizes = [q.weight.shape[0], k.weight.shape[0], v.weight.shape[0]]
+
+    def __call__(self, x, stream=None):
+        return torch.split(self.linear(x, stream), self.sizes, dim=-1)
+
+
 @dataclass
 class StackedExperts:
     """One projection of all experts: w [E, N, K*bits/32], s/b [E, N, K/gs]."""

@@ -42,6 +42,18 @@ def test_fused_mlp_matches_mlp():
         assert ((got - ref).abs().max() / ref.abs().max()).item() <= 1e-2
 
 
+def test_fused_qkv_matches_projections():
+    torch.manual_seed(3)
+    dt = torch.bfloat16
+    lin = lambda o, i: nn.QuantizedLinear(*_q((torch.randn(o, i, device="cuda") * 0.02).to(dt)), 64, 4)
+    q, k, v = lin(512, 1024), lin(128, 1024), lin(128, 1024)
+    f = nn.FusedQKV(q, k, v)
+    for M in (1, 7):
+        x = torch.randn(M, 1024, device="cuda").to(dt)
+        for got, ref in zip(f(x), (q(x), k(x), v(x))):
+            assert ((got.float() - ref.float()).abs().max() / ref.float().abs().max()).item() <= 1e-2
+
+
 @pytest.mark.parametrize("fused", [False, True])
 def test_moe_matches_per_expert_loop(fused):
     torch.manual_seed(1)
