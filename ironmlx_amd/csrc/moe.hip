@@ -116,9 +116,19 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(const int32_t* experts, 
     }
     keys[i] = key;
   }
+  // A pass with stride <= 64 pairs elements inside 128-element windows that
+  // one wave owns (pairs i = 64 w .. 64 w + 63, and i + 1024 j), so it needs a
+  // workgroup barrier only after a pass (or the load) that crossed windows.
+  bool cross = true;
   for (int size = 2; size <= np; size <<= 1) {
     for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      __syncthreads();
+      if (cross || stride >= 128) {
+        __syncthreads();
+      } else {
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+      }
+      cross = stride >= 128;
       for (int i = tid; i < (np >> 1); i += 1024) {
         const int lo = 2 * i - (i & (stride - 1));
         const int hi = lo + stride;
