@@ -441,6 +441,11 @@ def bench_fused(ops, Ms=(1, 4, 16), layers=32):
         tg = _graph_layers([lambda: ops.dequantize_rows(ew, es, eb, tok, 64, 4)], reps=10)
         tf = _graph_layers([lambda: ops.dequantize(ew, es, eb, 64, 4).index_select(0, tok)], reps=3)
         emb[str(T)] = {"row_gather_us": round(tg * 1e6, 2), "full_table_dequant_us": round(tf * 1e6, 2)}
+    # dequantize alone: packed codes + scales / biases in, bf16 out
+    td = _graph_layers([lambda: ops.dequantize(ew, es, eb, 64, 4)], reps=5)
+    dbytes = V * Hd // 2 + V * (Hd // 64) * 4 + V * Hd * 2
+    emb["dequantize_table"] = {"us": round(td * 1e6, 2), "gbs": round(dbytes / td / 1e9, 1),
+                               "hbm_frac": round(dbytes / td / 1e9 / HBM_PEAK_GBS, 3)}
     out["embedding_lookup_vocab128256_h4096"] = emb
     del ew, es, eb
     torch.cuda.empty_cache()

@@ -54,21 +54,29 @@ __global__ __launch_bounds__(256) void dequant_kernel(ConvArgs a, int64_t nchunk
   }
   const int gs = AFF ? a.gs : ModeInfo<MODE>::GS;
   const int G = K / gs;
+  // a 32-code chunk lies in one group (affine and MX group sizes are multiples
+  // of 32); nvfp4's 16-code groups give two per chunk: scales load once per chunk
+  const int64_t g0 = row * G + k0 / gs;
+  float s0, b0 = 0.f, s1;
+  if constexpr (AFF) {
+    using SS = typename Store<SDT>::T;
+    s0 = s1 = to_f<SDT>(static_cast<const SS*>(a.s)[g0]);
+    b0 = to_f<SDT>(static_cast<const SS*>(a.b)[g0]);
+  } else {
+    const uint8_t* s8 = static_cast<const uint8_t*>(a.s);
+    s0 = fp_scale<MODE>(s8[g0]);
+    s1 = (MODE == NVFP4 && k0 + 16 < K) ? fp_scale<MODE>(s8[g0 + 1]) : s0;
+  }
   OS vals[32];
 #pragma unroll
   for (int j = 0; j < 32; ++j) {
-    const int k = k0 + j;
-    const int64_t gi = row * G + (k < K ? k : K - 1) / gs;
     const uint32_t q = chunk_code<BITS>(wd, j);
     float v;
     if constexpr (AFF) {
-      using SS = typename Store<SDT>::T;
-      const float s = to_f<SDT>(static_cast<const SS*>(a.s)[gi]);
-      const float b = to_f<SDT>(static_cast<const SS*>(a.b)[gi]);
-      const float p = s * static_cast<float>(q);
-      v = p + b;
+      const float p = s0 * static_cast<float>(q);
+      v = p + b0;
     } else {
-      v = fp_elem<MODE>(q) * fp_scale<MODE>(static_cast<const uint8_t*>(a.s)[gi]);
+      v = fp_elem<MODE>(q) * (j < 16 ? s0 : s1);
     }
     vals[j] = from_f<ODT>(v);
   }
