@@ -196,6 +196,7 @@ hipError_t fill_zero(void* p, int dt, int64_t n, hipStream_t st) {
 // choose the kernel family for one problem
 hipError_t run_qmm(QmmArgs& a) {
   if (qmv_q4_m1_supported(a)) return launch_qmv_q4_m1(a);
+  if (qmv_q8_m1_supported(a)) return launch_qmv_q8_m1(a);
   if (a.nbatch <= 65535 && qmm_skinny_fac_supported(a)) return launch_qmm_skinny_fac(a);
   if (a.M >= 2 && a.M <= 64 && a.nbatch * ((a.M + 31) / 32) <= 65535 && qmm_skinny_supported(a))
     return launch_qmm_skinny(a);

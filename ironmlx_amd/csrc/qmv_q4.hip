@@ -18,6 +18,7 @@
 // xs = sum x over the chunk (one quantization group):
 //   s * sum(x q) + b * xs = s * (d - C * xs) + b * xs.
 #include "launch.h"
+#include "mfma_common.h"
 
 namespace iqmm {
 
@@ -431,6 +432,164 @@ hipError_t launch_xt(const QmmArgs& a) {
 
 hipError_t launch_qmv_q4_m1(const QmmArgs& a) {
   return a.xdt == BF16 ? launch_xt<BF16>(a) : launch_xt<F16>(a);
+}
+
+}  // namespace iqmm
+
+// ---------------------------------------------------------------------------
+// M = 1 GEMV for 8-bit codes: affine 8-bit and mxfp8 (transpose).  Same load
+// plan as the 4-bit kernel, in 16-code half chunks: lane l owns half chunks
+// l, l + 64, ... of every row, so each weight load is a contiguous 1 KiB per
+// wave, and every load is issued before any arithmetic.  x (cache-resident)
+// is converted to fp32 once per lane and shared by the RB rows; a code becomes
+// fp32 with one v_cvt_f32_ubyte (affine) or a 16-bit e4m3 -> fp16 bit move and
+// v_cvt_f32_f16 (mxfp8: e4m3 / 256 exactly; the 256 is folded into the group
+// scale).  Affine groups are rescaled per half chunk as s . sum x q + b . sum x.
+namespace iqmm {
+
+template <int XT, int RB, int HPL, int MODE>
+__global__ __launch_bounds__(64) void qmv_q8_kernel(Q4Args p) {
+  using XS = uint16_t;
+  constexpr bool AFF = MODE == AFFINE;
+  const int lane = threadIdx.x;
+  const int N = p.N, K = p.K, H = K >> 4;
+  XS* out = reinterpret_cast<XS*>(p.out);
+  const int row0 = blockIdx.x * RB;
+  const uint32_t wrow = static_cast<uint32_t>(K);
+  const uint32_t srow = AFF ? (static_cast<uint32_t>(K) >> p.gshift) * 2 : static_cast<uint32_t>(K) >> 5;
+
+  uint32_t hw[HPL], hx[HPL], hg[HPL];
+#pragma unroll
+  for (int j = 0; j < HPL; ++j) {
+    const uint32_t h = static_cast<uint32_t>(min(lane + 64 * j, H - 1));
+    hw[j] = h << 4;
+    hx[j] = h << 5;
+    hg[j] = AFF ? ((h << 4) >> p.gshift) * 2 : (h >> 1);
+  }
+  // 1. x half chunks (16 values, 32 bytes) first
+  u32x4_t xv[HPL][2];
+#pragma unroll
+  for (int j = 0; j < HPL; ++j)
+#pragma unroll
+    for (int i = 0; i < 2; ++i) xv[j][i] = *reinterpret_cast<const u32x4_t*>(p.x + hx[j] + 16 * i);
+  // 2. per row: weight half chunks, then scales / biases
+  u32x4_t wv[RB][HPL];
+  XS sr[RB][HPL], br[RB][HPL];
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    const uint32_t row = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(min(row0 + r, N - 1)));
+    const char* wr = p.w + row * wrow;
+#pragma unroll
+    for (int j = 0; j < HPL; ++j) wv[r][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(wr + hw[j]));
+#pragma unroll
+    for (int j = 0; j < HPL; ++j) {
+      if constexpr (AFF) {
+        sr[r][j] = *reinterpret_cast<const XS*>(p.s + row * srow + hg[j]);
+        br[r][j] = *reinterpret_cast<const XS*>(p.b + row * srow + hg[j]);
+      } else {
+        sr[r][j] = *reinterpret_cast<const uint8_t*>(p.s + row * srow + hg[j]);
+      }
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // 3. x to fp32 (and its half-chunk sums for the affine bias term)
+  float xf[HPL][16], xsum[HPL];
+#pragma unroll
+  for (int j = 0; j < HPL; ++j) {
+    const uint32_t w8[8] = {xv[j][0].x, xv[j][0].y, xv[j][0].z, xv[j][0].w,
+                            xv[j][1].x, xv[j][1].y, xv[j][1].z, xv[j][1].w};
+    float sacc = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      xf[j][2 * i] = to_f<XT>(static_cast<XS>(w8[i] & 0xffffu));
+      xf[j][2 * i + 1] = to_f<XT>(static_cast<XS>(w8[i] >> 16));
+      sacc += xf[j][2 * i] + xf[j][2 * i + 1];
+    }
+    xsum[j] = lane + 64 * j < H ? sacc : 0.f;
+  }
+  // 4. rows in load order
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    float acc = 0.f;
+#pragma unroll
+    for (int j = 0; j < HPL; ++j) {
+      const uint32_t wd[4] = {wv[r][j].x, wv[r][j].y, wv[r][j].z, wv[r][j].w};
+      float d = 0.f;
+      bool nan = false;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if constexpr (AFF) {
+          d = fmaf(xf[j][4 * q + 0], ubyte_f<0>(wd[q]), d);
+          d = fmaf(xf[j][4 * q + 1], ubyte_f<1>(wd[q]), d);
+          d = fmaf(xf[j][4 * q + 2], ubyte_f<2>(wd[q]), d);
+          d = fmaf(xf[j][4 * q + 3], ubyte_f<3>(wd[q]), d);
+        } else {
+          // bytes 0, 2 and 1, 3 spread to 16-bit lanes: e4m3 -> fp16 bits of e4m3 / 256
+          const uint32_t even = wd[q] & 0x00ff00ffu, odd = (wd[q] >> 8) & 0x00ff00ffu;
+          const uint32_t he = ((even & 0x007f007fu) << 7) | ((even & 0x00800080u) << 8);
+          const uint32_t ho = ((odd & 0x007f007fu) << 7) | ((odd & 0x00800080u) << 8);
+          d = fmaf(xf[j][4 * q + 0], h_to_f(static_cast<uint16_t>(he)), d);
+          d = fmaf(xf[j][4 * q + 1], h_to_f(static_cast<uint16_t>(ho)), d);
+          d = fmaf(xf[j][4 * q + 2], h_to_f(static_cast<uint16_t>(he >> 16)), d);
+          d = fmaf(xf[j][4 * q + 3], h_to_f(static_cast<uint16_t>(ho >> 16)), d);
+          // S.1111.111 codes are NaN
+          nan = nan || ((((wd[q] & 0x7f7f7f7fu) + 0x01010101u) & 0x80808080u) != 0u);
+        }
+      }
+      if (lane + 64 * j >= H) d = 0.f;
+      if constexpr (AFF) {
+        acc = fmaf(to_f<XT>(sr[r][j]), d, fmaf(to_f<XT>(br[r][j]), xsum[j], acc));
+      } else {
+        const float sc = fp_scale<MODE>(sr[r][j]) * 256.0f;
+        acc = fmaf(sc, nan && lane + 64 * j < H ? __builtin_nanf("") : d, acc);
+      }
+    }
+    const float v = dpp_sum_to_lane63(acc);
+    if (lane == 63 && row0 + r < N) out[row0 + r] = from_f<XT>(v);
+  }
+}
+
+bool qmv_q8_m1_supported(const QmmArgs& a) {
+  // 1..8 half chunks per lane (K in [1024, 8192], K % 16 == 0); one matrix below 4 GiB
+  const bool mode_ok = (a.mode == AFFINE && a.bits == 8) || a.mode == MXFP8;
+  return a.transpose && a.M == 1 && !a.glu && mode_ok && (a.xdt == BF16 || a.xdt == F16) && a.nbatch == 1 &&
+         a.bm.ndim == 0 && a.bm.lhs == nullptr && a.bm.rhs == nullptr && a.K % 16 == 0 && a.K >= 1024 &&
+         a.K <= 8192 && static_cast<int64_t>(a.N) * a.K < (int64_t{1} << 32);
+}
+
+namespace {
+template <int XT, int RB, int HPL>
+hipError_t q8_launch(const QmmArgs& a, const Q4Args& p) {
+  const dim3 grid(static_cast<unsigned>((a.N + RB - 1) / RB));
+  if (a.mode == MXFP8) hipLaunchKernelGGL((qmv_q8_kernel<XT, RB, HPL, MXFP8>), grid, dim3(64), 0, a.stream, p);
+  else hipLaunchKernelGGL((qmv_q8_kernel<XT, RB, HPL, AFFINE>), grid, dim3(64), 0, a.stream, p);
+  return hipGetLastError();
+}
+template <int XT>
+hipError_t q8_launch_x(const QmmArgs& a, const Q4Args& p) {
+  // rows per wave as the 4-bit kernel: 2 from 4096 rows, 1 below
+  const bool two = a.N >= 4096;
+  switch ((((a.K >> 4) + 63) / 64 + 1) / 2 * 2) {  // half chunks per lane, rounded up to even
+    case 2: return two ? q8_launch<XT, 2, 2>(a, p) : q8_launch<XT, 1, 2>(a, p);
+    case 4: return two ? q8_launch<XT, 2, 4>(a, p) : q8_launch<XT, 1, 4>(a, p);
+    case 6: return two ? q8_launch<XT, 2, 6>(a, p) : q8_launch<XT, 1, 6>(a, p);
+    default: return two ? q8_launch<XT, 2, 8>(a, p) : q8_launch<XT, 1, 8>(a, p);
+  }
+}
+}  // namespace
+
+hipError_t launch_qmv_q8_m1(const QmmArgs& a) {
+  if (a.N <= 0) return hipSuccess;
+  Q4Args p{};
+  p.x = static_cast<const char*>(a.x);
+  p.w = reinterpret_cast<const char*>(a.w);
+  p.s = static_cast<const char*>(a.s);
+  p.b = static_cast<const char*>(a.b);
+  p.out = static_cast<char*>(a.out);
+  p.N = a.N;
+  p.K = a.K;
+  p.gshift = a.mode == AFFINE ? __builtin_ctz(a.gs) : 0;
+  return a.xdt == BF16 ? q8_launch_x<BF16>(a, p) : q8_launch_x<F16>(a, p);
 }
 
 }  // namespace iqmm

@@ -412,3 +412,43 @@ def test_gather_qmm_sorted_many_rows_per_expert(ops, mode):
                          True, None if mode != "affine" else 64, None if mode != "affine" else 4, mode,
                          odt="f32")
         assert rel_err(g[i], ref) <= (TOL if mode == "affine" else TOL_FP)["f16"]
+
+
+# ------------------------------------------------------------------ 8-bit M = 1 GEMV
+@pytest.mark.parametrize("xdt", ["bf16", "f16"])
+@pytest.mark.parametrize("mode,gs", [("affine", 32), ("affine", 64), ("affine", 128), ("mxfp8", 32)])
+@pytest.mark.parametrize("N,K", [(300, 1024), (4100, 4096), (97, 3072), (2048, 8192), (64, 1056)])
+def test_qmv_8bit_gemv(ops, xdt, mode, gs, N, K):
+    """qmv_q8_kernel: affine 8-bit and mxfp8 at M = 1 (16-code half chunks per
+    lane; partial last slots when K / 16 is not a multiple of 64)."""
+    if K % gs:
+        pytest.skip("K not a multiple of the group size")
+    print(f"q8 gemv {mode} gs{gs} {xdt} N={N} K={K}", flush=True)
+    rng = np.random.default_rng(N + K + gs)
+    if mode == "affine":
+        w, s, b = rand_affine(rng, N, K, gs, 8, xdt)
+        ts, tb = from_np(s, xdt), from_np(b, xdt)
+    else:
+        w, s = rand_fp(rng, N, K, mode)
+        ts, tb, b = torch.from_numpy(s).cuda(), None, None
+    x = oracle.from_float(rng.standard_normal((1, K)).astype(np.float32), xdt)
+    got = ops.quantized_matmul(from_np(x, xdt), words_to_torch(w), ts, tb, True,
+                               gs if mode == "affine" else None, 8 if mode == "affine" else None, mode)
+    ref = oracle.qmm(x, xdt, w, s, b, xdt if mode == "affine" else "f32", True,
+                     gs if mode == "affine" else None, 8 if mode == "affine" else None, mode)
+    tol = TOL if mode == "affine" else TOL_FP
+    assert rel_err(as_f64(to_np(got, xdt), xdt), as_f64(ref, xdt)) <= tol[xdt]
+
+
+def test_qmv_mxfp8_nan_code(ops):
+    """An e4m3 NaN code (S.1111.111) makes its row NaN, as the dequantized
+    weight is NaN; other rows are unaffected."""
+    rng = np.random.default_rng(3)
+    N, K = 8, 2048
+    w, s = rand_fp(rng, N, K, "mxfp8")
+    w = w.copy()
+    w[5, 100] = (w[5, 100] & ~np.uint32(0xff)) | np.uint32(0x7f)
+    x = oracle.from_float(rng.standard_normal((1, K)).astype(np.float32), "bf16")
+    got = ops.quantized_matmul(from_np(x, "bf16"), words_to_torch(w), torch.from_numpy(s).cuda(), None, True,
+                               mode="mxfp8").float().cpu().numpy()
+    assert np.isnan(got[0, 5]) and not np.isnan(np.delete(got[0], 5)).any()
