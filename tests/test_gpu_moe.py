@@ -197,3 +197,49 @@ def test_moe_combine_bit_exact(ops, dt, T, k, E, D):
     ref = oracle.moe_combine(to_np(y, dt).reshape(T * k, D), dt, inv.cpu().numpy(), experts.cpu().numpy(),
                              scores.cpu().numpy(), E)
     assert np.array_equal(got.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+
+
+# ------------------------------------------------------------------ edge cases
+def test_moe_empty_and_single(ops):
+    """T = 0 tokens (empty outputs, zero offsets), E = 1 / k = 1, and a combine
+    width that is not a multiple of the 256-column workgroup."""
+    lg = torch.zeros((0, 256), dtype=torch.bfloat16, device="cuda")
+    sc, ex = ops.moe_route(lg, 8, True)
+    assert sc.shape == (0, 8) and ex.shape == (0, 8)
+    tok, srt, inv, off = ops.moe_sort(ex, 256)
+    assert tok.numel() == 0 and torch.equal(off.cpu(), torch.zeros(257, dtype=torch.int32))
+    y = torch.zeros((0, 1, 64), dtype=torch.bfloat16, device="cuda")
+    assert ops.moe_combine(y, inv, ex, sc, 256).shape == (0, 64)
+
+    lg1 = torch.randn((5, 1), device="cuda").to(torch.bfloat16)
+    sc1, ex1 = ops.moe_route(lg1, 1, True)
+    assert torch.equal(ex1.cpu(), torch.zeros((5, 1), dtype=torch.int32))
+    assert torch.equal(sc1.cpu(), torch.ones((5, 1)))
+
+    rng = np.random.default_rng(4)
+    T, k, E, D = 9, 3, 16, 1000
+    lgn = oracle.from_float(rng.standard_normal((T, E)).astype(np.float32), "bf16")
+    sc2, ex2 = ops.moe_route(from_np(lgn, "bf16"), k, False)
+    _, _, inv2, _ = ops.moe_sort(ex2, E)
+    y2 = torch.randn((T * k, D), generator=torch.Generator().manual_seed(1)).to(torch.bfloat16).cuda()
+    got = ops.moe_combine(y2, inv2, ex2, sc2, E)
+    ref = oracle.moe_combine(to_np(y2, "bf16"), "bf16", inv2.cpu().numpy(), ex2.cpu().numpy(),
+                             sc2.cpu().numpy(), E)
+    assert np.array_equal(got.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+
+
+def test_fused_and_gather_empty(ops):
+    rng = np.random.default_rng(6)
+    w, s, b = rand_affine(rng, 2 * 96, 1024, 64, 4, "bf16")
+    tw, ts, tb = words_to_torch(w), from_np(s, "bf16"), from_np(b, "bf16")
+    x0 = torch.zeros((0, 1024), dtype=torch.bfloat16, device="cuda")
+    assert ops.quantized_swiglu(x0, tw, ts, tb).shape == (0, 96)
+    idx0 = torch.zeros((0,), dtype=torch.int32, device="cuda")
+    assert ops.dequantize_rows(tw, ts, tb, idx0).shape == (0, 1024)
+    # odd I: the last GEMV wave holds a single output
+    w3, s3, b3 = rand_affine(rng, 2 * 97, 1024, 64, 4, "bf16")
+    x1 = torch.randn((1, 1024), generator=torch.Generator().manual_seed(2)).to(torch.bfloat16).cuda()
+    got = ops.quantized_swiglu(x1, words_to_torch(w3), from_np(s3, "bf16"), from_np(b3, "bf16"))
+    gu = ops.quantized_matmul(x1, words_to_torch(w3), from_np(s3, "bf16"), from_np(b3, "bf16"), True)
+    ref = oracle.swiglu(to_np(gu, "bf16"), "bf16")
+    assert np.array_equal(_bits(got, "bf16"), np.ascontiguousarray(ref).view(np.uint16))
