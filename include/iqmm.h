@@ -222,8 +222,10 @@ int iqmm_moe_sort(iqmm_array* res_tokens, iqmm_array* res_sorted, iqmm_array* re
  * Weighted combine of expert outputs: out[t, :] = sum over the k slots of t,
  * in ascending expert order, of float32(y[inverse[t*k + slot], :]) * score,
  * accumulated sequentially in float32 as mlx/src/nn/moe.rs:146-168 does.
- *   y        [n, D] (or [n, 1, D]) float32 | float16 | bfloat16, sorted rows
- *   inverse  [T, k] or [n] int32 from iqmm_moe_sort
+ *   y        [n, D] (or [n, 1, D]) float32 | float16 | bfloat16 expert rows in
+ *            any order (sorted by iqmm_moe_sort, or one row per (token, slot))
+ *   inverse  [T, k] or [n] int32: the row of y of each (token, slot)
+ *            (iqmm_moe_sort's inverse, or 0 .. n-1 for unsorted rows)
  *   experts  [T, k] int32, scores [T, k] float32 from iqmm_moe_route
  *   res      [T, D] float32
  * Slots whose expert is outside [0, num_experts) are skipped, as the

@@ -155,10 +155,11 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(const int32_t* experts, 
   }
 }
 
-// out[t, d] = sum over t's valid slots in ascending sorted position (=
-// ascending expert) of float(y[pos, d]) * score.  One workgroup per token:
-// the k slots are ranked by position once (in LDS), then each thread runs the
-// ordered sum for its column (blockIdx.y picks 256 columns).
+// out[t, d] = sum over t's valid slots in ascending expert order of
+// float(y[pos, d]) * score.  One workgroup per token: the k slots are ranked
+// once (in LDS), then each thread runs the ordered sum for its column
+// (blockIdx.y picks 256 columns).  Rows may be in any order in y (sorted by
+// expert, or one row per (token, slot) when the sort is skipped).
 template <int DT>
 __global__ __launch_bounds__(256) void moe_combine_kernel(const typename Store<DT>::T* y, const int32_t* inverse,
                                                           const int32_t* experts, const float* scores, float* out,
@@ -175,13 +176,14 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const typename Store<D
       const int pos = inverse[base + tid];
       const int e = experts[base + tid];
       const bool ok = pos >= 0 && pos < n && e >= 0 && e < E;
-      // rank among the valid slots by sorted position (slot order breaks ties,
-      // so ranks stay distinct even for repeated positions)
+      // rank among the valid slots by expert id, then row position, then slot
+      // (distinct ranks; for sorted rows the position order is the expert order)
       int rank = 0;
       for (int j = 0; j < k; ++j) {
         const int pj = inverse[base + j], ej = experts[base + j];
         const bool okj = pj >= 0 && pj < n && ej >= 0 && ej < E;
-        rank += (okj && (pj < pos || (pj == pos && j < tid))) ? 1 : 0;
+        const bool before = ej < e || (ej == e && (pj < pos || (pj == pos && j < tid)));
+        rank += (okj && before) ? 1 : 0;
       }
       if (ok) {
         rowoff[rank] = static_cast<int64_t>(pos) * D;

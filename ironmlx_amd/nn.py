@@ -275,21 +275,39 @@ class MoEMLP:
         logits = self.gate(x_flat).contiguous()
         return ops.moe_route(logits, self.k, self.norm_topk_prob, stream)
 
+    # at most this many (token, slot) rows skip the sort: every row is its own
+    # GEMV (the grouped kernel has nothing to share), so rows stay in (token,
+    # slot) order and the index maps are fixed per token count
+    UNSORTED_ROWS = 16
+
+    def _identity_maps(self, n, device):
+        key = (n, device)
+        cache = self.__dict__.setdefault("_maps", {})
+        if key not in cache:
+            rows = torch.arange(n * self.k, device=device, dtype=torch.int32)
+            cache[key] = ((rows // self.k).contiguous(), rows)
+        return cache[key]
+
     def experts_forward(self, x_flat, scores, idx, stream=None):
         n, d = x_flat.shape
         E = self.num_experts()
         idx = idx.to(torch.int32).contiguous()
-        tokens, rhs, inverse, _ = ops.moe_sort(idx, E, stream)
+        if n * self.k <= self.UNSORTED_ROWS:
+            tokens, inverse = self._identity_maps(n, x_flat.device)
+            rhs, srt = idx.reshape(-1), False
+        else:
+            tokens, rhs, inverse, _ = ops.moe_sort(idx, E, stream)
+            srt = True
         x3 = x_flat.reshape(n, 1, d).contiguous()
         if "gate_up" in self.experts:
             gu = self.experts["gate_up"]
             h = ops.gather_qmm_swiglu(x3, gu.weight, gu.scales, gu.biases, tokens, rhs,
-                                      gu.group_size, gu.bits, gu.mode, True, stream)
+                                      gu.group_size, gu.bits, gu.mode, srt, stream)
         else:
-            g = _gqmm(x3, self.experts["gate"], rhs, tokens, stream=stream)
-            u = _gqmm(x3, self.experts["up"], rhs, tokens, stream=stream)
+            g = _gqmm(x3, self.experts["gate"], rhs, tokens, srt, stream=stream)
+            u = _gqmm(x3, self.experts["up"], rhs, tokens, srt, stream=stream)
             h = (F.silu(g) * u).contiguous()
-        y = _gqmm(h, self.experts["down"], rhs, stream=stream)
+        y = _gqmm(h, self.experts["down"], rhs, sorted_indices=srt, stream=stream)
         return ops.moe_combine(y, inverse, idx, scores.contiguous(), E, stream)
 
     def __call__(self, x, stream=None):

@@ -243,3 +243,18 @@ def test_fused_and_gather_empty(ops):
     gu = ops.quantized_matmul(x1, words_to_torch(w3), from_np(s3, "bf16"), from_np(b3, "bf16"), True)
     ref = oracle.swiglu(to_np(gu, "bf16"), "bf16")
     assert np.array_equal(_bits(got, "bf16"), np.ascontiguousarray(ref).view(np.uint16))
+
+
+def test_moe_combine_unsorted_rows(ops):
+    """Rows in (token, slot) order with the identity inverse (the sort is
+    skipped for decode): still summed in ascending expert order."""
+    rng = np.random.default_rng(8)
+    T, k, E, D = 2, 8, 256, 2048
+    lg = oracle.from_float(rng.standard_normal((T, E)).astype(np.float32), "bf16")
+    scores, experts = ops.moe_route(from_np(lg, "bf16"), k, True)
+    inv = torch.arange(T * k, dtype=torch.int32, device="cuda")
+    y = torch.randn(T * k, 1, D, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16).cuda()
+    got = ops.moe_combine(y, inv, experts, scores, E)
+    ref = oracle.moe_combine(to_np(y, "bf16").reshape(T * k, D), "bf16", inv.cpu().numpy(),
+                             experts.cpu().numpy(), scores.cpu().numpy(), E)
+    assert np.array_equal(got.cpu().numpy().view(np.uint32), ref.view(np.uint32))
