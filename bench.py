@@ -202,12 +202,35 @@ def bench_moe(ops, Ts=(1, 64, 512), reps=10):
     return out
 
 
+_CAPTURE_STREAM = None
+
+
+def _capture_stream():
+    """One stream for every capture, warmed up before capturing: the library
+    keeps its per-stream workspaces (split-K partials, fused-SwiGLU product,
+    grouped-gather offsets), so captured calls reuse them instead of adding
+    allocation nodes to the graph."""
+    global _CAPTURE_STREAM
+    if _CAPTURE_STREAM is None:
+        _CAPTURE_STREAM = torch.cuda.Stream()
+    return _CAPTURE_STREAM
+
+
+def _warm_on_capture_stream(fn):
+    s = _capture_stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    s.synchronize()
+
+
 def graph_time(fn, n):
     """Average device time of fn() over n calls captured in one HIP graph."""
     fn()
+    _warm_on_capture_stream(fn)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+    with torch.cuda.graph(g, stream=_capture_stream()):
         for _ in range(n):
             fn()
     g.replay()
@@ -331,9 +354,10 @@ def _graph_layers(fns, reps=5):
         for f in fns:
             f()
     step()
+    _warm_on_capture_stream(step)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+    with torch.cuda.graph(g, stream=_capture_stream()):
         step()
     g.replay()
     torch.cuda.synchronize()

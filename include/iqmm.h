@@ -40,12 +40,18 @@
  * the inferred ones.  Inputs are never modified or freed.  Work is enqueued on
  * `stream` (a hipStream_t; NULL = the null stream) and is complete after the
  * stream is synchronised, as after mlx's `eval` (mlx/src/array.rs:111-113).
- * The library's device allocations are workspaces taken with hipMallocAsync
- * and released with hipFreeAsync on `stream` (stream-ordered, capturable in
- * a HIP graph): the fp32 partial sums of a split-K GEMM (few output tiles,
- * M > 64), the gate_up product of a fused SwiGLU outside its fused kernels,
- * and the expert segment offsets of a sorted grouped gather_qmm.  Calls are
- * re-entrant; calls on one stream execute in order.
+ * Scratch memory: the fp32 partial sums of a split-K GEMM (few output tiles,
+ * M > 64), the gate_up product of a fused SwiGLU outside its fused kernels and
+ * the expert segment offsets of a sorted grouped gather_qmm live in per-stream
+ * workspaces: one grow-only buffer per (device, stream, use), taken from the
+ * stream-ordered pool (hipMallocAsync on `stream`) and kept until the process
+ * ends, so HIP graphs captured on a stream keep valid pointers and need no
+ * allocation nodes.  A capture on a stream whose buffer is too small (no
+ * eager call on that stream yet) falls back to a hipMallocAsync /
+ * hipFreeAsync pair inside the graph.  Calls are re-entrant across streams;
+ * calls on one stream execute in order and share its workspaces, so a graph
+ * must not be replayed concurrently with other library work on the stream it
+ * was captured on.
  */
 #ifndef IQMM_H
 #define IQMM_H

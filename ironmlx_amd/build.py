@@ -15,7 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libiqmm.so")
-SOURCES = ["api.hip", "qmv.hip", "qmv_q4.hip", "qmm_mfma.hip", "qmm_gemm.hip", "qmm_skinny.hip", "convert.hip", "moe.hip"]
+SOURCES = ["api.hip", "qmv.hip", "qmv_q4.hip", "qmm_mfma.hip", "qmm_gemm.hip", "qmm_skinny.hip", "convert.hip", "moe.hip", "workspace.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",

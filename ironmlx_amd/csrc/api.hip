@@ -214,7 +214,8 @@ int elt_size(int dt) { return dt == IQMM_FLOAT32 ? 4 : 2; }
 // workgroup; both apply the SwiGLU in their epilogue.  Every other shape
 // computes the [.., M, 2I] product
 // into a stream-ordered workspace with the regular kernels (`product`) and
-// then runs the elementwise SwiGLU over it.
+// then runs the elementwise SwiGLU over it (the product lives in the
+// stream's GLU workspace, workspace.hip).
 template <class F>
 hipError_t run_glu(QmmArgs& a, bool try_fused, F&& product) {
   a.glu = 1;
@@ -224,13 +225,14 @@ hipError_t run_glu(QmmArgs& a, bool try_fused, F&& product) {
   const int64_t I = a.N, rows = a.nbatch * a.M;
   void* out = a.out;
   void* ws = nullptr;
-  hipError_t e = hipMallocAsync(&ws, static_cast<size_t>(rows) * 2 * I * elt_size(a.xdt), a.stream);
+  bool owned = false;
+  hipError_t e = workspace_get(a.stream, WS_GLU, static_cast<size_t>(rows) * 2 * I * elt_size(a.xdt), &ws, &owned);
   if (e != hipSuccess) return e;
   a.N = static_cast<int>(2 * I);
   a.out = ws;
   e = product(a);
   if (e == hipSuccess) e = launch_swiglu_rows(ws, out, rows, I, a.xdt, a.stream);
-  const hipError_t f = hipFreeAsync(ws, a.stream);
+  const hipError_t f = owned ? hipFreeAsync(ws, a.stream) : hipSuccess;
   a.N = static_cast<int>(I);
   a.out = out;
   return e != hipSuccess ? e : f;

@@ -983,16 +983,16 @@ hipError_t set_lds_once(size_t bytes) {
 }
 
 // Run `launch(part)` into an fp32 workspace of ks partial outputs and sum
-// them into a.out in a fixed order.  The workspace is stream-ordered
-// (hipMallocAsync / hipFreeAsync), so concurrent calls on other streams get
-// their own.
+// them into a.out in a fixed order.  The workspace is the stream's split-K
+// buffer (workspace.hip), so concurrent calls on other streams get their own.
 template <int XT, class F>
 hipError_t splitk_run(const QmmArgs& a, int ks, F&& launch) {
   const int64_t n = static_cast<int64_t>(a.nbatch) * a.M * a.N;
-  float* part = nullptr;
-  hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&part), static_cast<size_t>(n) * ks * sizeof(float),
-                                a.stream);
+  void* ws = nullptr;
+  bool owned = false;
+  hipError_t e = workspace_get(a.stream, WS_SPLITK, static_cast<size_t>(n) * ks * sizeof(float), &ws, &owned);
   if (e != hipSuccess) return e;
+  float* part = static_cast<float*>(ws);
   e = launch(part);
   if (e == hipSuccess) {
     const int64_t nb = (n + 1023) / 1024;
@@ -1000,7 +1000,7 @@ hipError_t splitk_run(const QmmArgs& a, int ks, F&& launch) {
                        static_cast<uint16_t*>(a.out), n, ks);
     e = hipGetLastError();
   }
-  const hipError_t f = hipFreeAsync(part, a.stream);
+  const hipError_t f = owned ? hipFreeAsync(part, a.stream) : hipSuccess;
   return e != hipSuccess ? e : f;
 }
 
@@ -1021,8 +1021,8 @@ hipError_t wr_launch_tile(const QmmArgs& a, int ks, float* part) {
 
 // Tile / split choice for the register-B kernel: 256 x 256 tiles while they
 // give most CUs a tile; otherwise 128 x 128 tiles with K split over enough
-// workgroups to fill the GPU.  Split partials are fp32 in a stream-ordered
-// workspace (hipMallocAsync / hipFreeAsync) summed in a fixed order by
+// workgroups to fill the GPU.  Split partials are fp32 in the stream's
+// split-K workspace (workspace.hip), summed in a fixed order by
 // splitk_reduce_kernel, so results do not depend on scheduling.
 template <int XT, int MODE, int BITS>
 hipError_t wr_launch(const QmmArgs& a, int G) {

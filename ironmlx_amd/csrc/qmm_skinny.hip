@@ -853,17 +853,18 @@ hipError_t launch_gather_sorted(const QmmArgs& a, int64_t nflat, int64_t E) {
   if (a.xdt != BF16 && a.xdt != F16) return hipErrorInvalidValue;
   if (a.N <= 0 || E <= 0 || nflat <= 0) return hipSuccess;
   if (E + 1 > 65535) return hipErrorInvalidConfiguration;
-  // segment offsets in a stream-ordered workspace (capturable in a HIP graph)
-  int64_t* off = nullptr;
-  hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&off), static_cast<size_t>(E + 1) * sizeof(int64_t),
-                                a.stream);
+  // segment offsets in the stream's offsets workspace (workspace.hip)
+  void* ws = nullptr;
+  bool owned = false;
+  hipError_t e = workspace_get(a.stream, WS_OFFSETS, static_cast<size_t>(E + 1) * sizeof(int64_t), &ws, &owned);
   if (e != hipSuccess) return e;
+  int64_t* off = static_cast<int64_t*>(ws);
   const int64_t nb = (nflat + 1 + 255) / 256;
   hipLaunchKernelGGL(segment_offsets_kernel, dim3(static_cast<unsigned>(nb)), dim3(256), 0, a.stream, a.bm.rhs,
                      a.bm.rhs_dt, nflat, E, off);
   e = hipGetLastError();
   if (e == hipSuccess) e = a.xdt == BF16 ? gather_by_mode<BF16>(a, nflat, E, off) : gather_by_mode<F16>(a, nflat, E, off);
-  const hipError_t f = hipFreeAsync(off, a.stream);
+  const hipError_t f = owned ? hipFreeAsync(off, a.stream) : hipSuccess;
   return e != hipSuccess ? e : f;
 }
 
