@@ -15,6 +15,8 @@
 // Reference op: mlx/src/ops.rs:695-727 with x = [B, 1, K] (one decode step
 // for B sequences, which mlx/src/generate/batch.rs:313-339 runs as B
 // separate M = 1 calls today).
+#include <type_traits>
+
 #include "launch.h"
 #include "mfma_common.h"
 
@@ -276,22 +278,33 @@ __global__ __launch_bounds__(64 * S) void qmm_skinny16_kernel(QmmArgs a, int nmt
 //   sum x (s q + b) = s D + (b - C s) X,
 // so per 128-code block a lane spends 7 VALU per 8 codes on unpacking and two
 // FMAs per accumulator on the group scale, instead of a full dequantization.
-// A groups-per-block split keeps every MFMA's sum inside one group: the 16
-// A rows are (x row, group-in-block) pairs, so a 16-row m tile holds
-// RPT = 16 / GB x rows (GB = 128 / gs groups per block), and the A rows of
-// the other group are zero in each k slot.  X comes from the same MFMA with
+// Every MFMA's sum must stay inside one group.  Without TR (used at gs 128,
+// one group per block) lane q's k slot is chunk 4p + q, and for GB = 128 / gs
+// groups per block the 16 A rows would be (x row, group-in-block) pairs with
+// RPT = 16 / GB x rows per m tile, the rows of the other group zero in each
+// k slot.  TR (gs 32 / 64) avoids those zero rows.  X comes from the same MFMA with
 // an all-ones B.  A wave covers NT 16-row weight tiles (x pairs and X are
 // shared by them) for the blocks [pb, pe) of K; the S waves of a workgroup
 // split K and their partial sums meet in LDS.
 // GLU (NT even): the weight holds 2N rows (gate [0, N), up [N, 2N)); tiles
 // [0, NT/2) of a workgroup are gate rows n0.. and tiles [NT/2, NT) the
 // matching up rows, and the epilogue writes silu(gate) * up for 8 NT columns.
-template <int XT, int NT, int MT, int GB, int S, int NB = 2, bool GLU = false>
+//
+// TR (chunk-major k slots): MFMA j of a block takes chunk 4p + j (32 codes,
+// one quantization group for gs >= 32) and lane (r, q) supplies its 8-code
+// piece q.  Every A row is then a live x row (RPT = 16), and the x pieces of
+// one load are 64 contiguous bytes per row.  The weights still arrive as one
+// 16-byte chunk per lane (lane q: chunk 4p + q) and a 4 x 4 dword transpose
+// across the lanes q (v_permlane32_swap, then v_permlane16_swap) turns them
+// into piece q of chunks 4p + 0..3.  The group scale then applies per MFMA
+// group: Y += s_g D_g + (b_g - C s_g) X_g.
+template <int XT, int NT, int MT, int GB, int S, int NB = 2, bool GLU = false, bool TR = false>
 __global__ __launch_bounds__(64 * S) void qmm_skinny_fac_kernel(QmmArgs a) {
   static_assert(!GLU || NT % 2 == 0, "GLU pairs gate tiles with up tiles");
   constexpr int NC = GLU ? 8 * NT : 16 * NT;  // output columns per workgroup
   using XS = uint16_t;
-  constexpr int RPT = 16 / GB;
+  constexpr int RPT = TR ? 16 : 16 / GB;
+  constexpr int GR = TR ? 1 : GB;  // groups summed in the epilogue
   constexpr float CM = XT == BF16 ? 128.f : 1024.f;
   constexpr uint32_t EB = XT == BF16 ? 0x43434343u : 0x64646464u;
   constexpr uint32_t ONE2 = XT == BF16 ? 0x3f803f80u : 0x3c003c00u;
@@ -326,7 +339,7 @@ __global__ __launch_bounds__(64 * S) void qmm_skinny_fac_kernel(QmmArgs a) {
 #pragma unroll
   for (int i = 0; i < MT; ++i) {
     const int m = i * RPT + r % RPT;
-    xlive[i] = (r / RPT == gq) && m < M;
+    xlive[i] = TR ? m < M : (r / RPT == gq) && m < M;
     xr[i] = x + (xlive[i] ? m : 0) * xrow;
   }
   const char* wr[NT];
@@ -343,24 +356,28 @@ __global__ __launch_bounds__(64 * S) void qmm_skinny_fac_kernel(QmmArgs a) {
   const int P = K >> 7;
   const int pb = (P * wave) / S, pe = (P * (wave + 1)) / S;
 
+  // TR: the GB group scales / biases of a block, one load each
+  using SG = typename std::conditional<!TR || GB == 1, XS, typename std::conditional<GB == 2, uint32_t, uint64_t>::type>::type;
   struct Blk {
     g_u32x4_t xa[MT][4];
     g_u32x4_t wv[NT];
-    XS sv[NT], bv[NT];
+    SG sv[NT], bv[NT];
   };
   auto load = [&](int p, Blk& B) {
-    const int c = 4 * min(p, pe - 1) + q;   // chunk of this lane's k slot
+    const int pc = min(p, pe - 1);
+    const int c = 4 * pc + q;   // chunk of this lane's weight load (and, without TR, its k slot)
 #pragma unroll
     for (int i = 0; i < MT; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        B.xa[i][j] = *reinterpret_cast<const g_u32x4_t*>(xr[i] + c * 64 + 16 * j);
-    const int go = ((c * 32) >> gshift) * 2;
+        B.xa[i][j] = TR ? *reinterpret_cast<const g_u32x4_t*>(xr[i] + (4 * pc + j) * 64 + 16 * q)
+                        : *reinterpret_cast<const g_u32x4_t*>(xr[i] + c * 64 + 16 * j);
+    const int go = TR ? ((pc * 128) >> gshift) * 2 : ((c * 32) >> gshift) * 2;
 #pragma unroll
     for (int tt = 0; tt < NT; ++tt) {
       B.wv[tt] = __builtin_nontemporal_load(reinterpret_cast<const g_u32x4_t*>(wr[tt] + c * 16));
-      B.sv[tt] = *reinterpret_cast<const XS*>(sr[tt] + go);
-      B.bv[tt] = *reinterpret_cast<const XS*>(br[tt] + go);
+      B.sv[tt] = *reinterpret_cast<const SG*>(sr[tt] + go);
+      B.bv[tt] = *reinterpret_cast<const SG*>(br[tt] + go);
     }
   };
   f32x4_t Y[NT][MT];
@@ -383,13 +400,36 @@ __global__ __launch_bounds__(64 * S) void qmm_skinny_fac_kernel(QmmArgs a) {
         A[i][j] = g_u32x4_t{__builtin_amdgcn_perm(v.z, v.x, 0x05040100u), __builtin_amdgcn_perm(v.z, v.x, 0x07060302u),
                             __builtin_amdgcn_perm(v.w, v.y, 0x05040100u), __builtin_amdgcn_perm(v.w, v.y, 0x07060302u)};
       }
-      X[i] = mfma16x<XT>(A[i][0], ones, f32x4_t{0.f, 0.f, 0.f, 0.f});
+      if constexpr (!TR) {
+        X[i] = mfma16x<XT>(A[i][0], ones, f32x4_t{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-      for (int j = 1; j < 4; ++j) X[i] = mfma16x<XT>(A[i][j], ones, X[i]);
+        for (int j = 1; j < 4; ++j) X[i] = mfma16x<XT>(A[i][j], ones, X[i]);
+      }
+    }
+    constexpr int JG = 4 / GB;  // TR: MFMAs per group
+    f32x4_t XG[TR ? MT : 1][TR ? GB : 1];
+    if constexpr (TR) {
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int g = 0; g < GB; ++g) {
+          XG[i][g] = mfma16x<XT>(A[i][g * JG], ones, f32x4_t{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+          for (int j = 1; j < JG; ++j) XG[i][g] = mfma16x<XT>(A[i][g * JG + j], ones, XG[i][g]);
+        }
     }
 #pragma unroll
     for (int tt = 0; tt < NT; ++tt) {
-      const uint32_t wd[4] = {B.wv[tt].x, B.wv[tt].y, B.wv[tt].z, B.wv[tt].w};
+      uint32_t wd[4] = {B.wv[tt].x, B.wv[tt].y, B.wv[tt].z, B.wv[tt].w};
+      if constexpr (TR) {
+        // 4 x 4 transpose over the lanes q = lane / 16: afterwards wd[j] of
+        // lane q is dword q of the chunk that lane j loaded (chunk 4p + j)
+        auto s02 = __builtin_amdgcn_permlane32_swap(wd[0], wd[2], false, false);
+        auto s13 = __builtin_amdgcn_permlane32_swap(wd[1], wd[3], false, false);
+        auto s01 = __builtin_amdgcn_permlane16_swap(s02[0], s13[0], false, false);
+        auto s23 = __builtin_amdgcn_permlane16_swap(s02[1], s13[1], false, false);
+        wd[0] = s01[0]; wd[1] = s01[1]; wd[2] = s23[0]; wd[3] = s23[1];
+      }
       g_u32x4_t Wp[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -398,7 +438,24 @@ __global__ __launch_bounds__(64 * S) void qmm_skinny_fac_kernel(QmmArgs a) {
         Wp[j] = g_u32x4_t{__builtin_amdgcn_perm(EB, lo, 0x04020400u), __builtin_amdgcn_perm(EB, hi, 0x04020400u),
                           __builtin_amdgcn_perm(EB, lo, 0x04030401u), __builtin_amdgcn_perm(EB, hi, 0x04030401u)};
       }
-      const float s = to_f<XT>(B.sv[tt]), b = to_f<XT>(B.bv[tt]);
+      if constexpr (TR) {
+#pragma unroll
+        for (int g = 0; g < GB; ++g) {
+          const float s = to_f<XT>(static_cast<XS>(B.sv[tt] >> (16 * g)));
+          const float b = to_f<XT>(static_cast<XS>(B.bv[tt] >> (16 * g)));
+          const float cb = fmaf(-CM, s, b);
+#pragma unroll
+          for (int i = 0; i < MT; ++i) {
+            f32x4_t D = mfma16x<XT>(A[i][g * JG], Wp[g * JG], f32x4_t{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+            for (int j = 1; j < JG; ++j) D = mfma16x<XT>(A[i][g * JG + j], Wp[g * JG + j], D);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) Y[tt][i][v] = fmaf(s, D[v], fmaf(cb, XG[i][g][v], Y[tt][i][v]));
+          }
+        }
+        continue;
+      }
+      const float s = to_f<XT>(static_cast<XS>(B.sv[tt])), b = to_f<XT>(static_cast<XS>(B.bv[tt]));
       const float cb = fmaf(-CM, s, b);
 #pragma unroll
       for (int i = 0; i < MT; ++i) {
@@ -445,7 +502,7 @@ __global__ __launch_bounds__(64 * S) void qmm_skinny_fac_kernel(QmmArgs a) {
 #pragma unroll
         for (int w2 = 0; w2 < S; ++w2)
 #pragma unroll
-          for (int g = 0; g < GB; ++g) acc[h] += red[((w2 * NT + tt) * MT + i) * 256 + (mr + RPT * g) * 16 + (nn & 15)];
+          for (int g = 0; g < GR; ++g) acc[h] += red[((w2 * NT + tt) * MT + i) * 256 + (mr + RPT * g) * 16 + (nn & 15)];
       }
       if (n0 + nn < N) out[static_cast<int64_t>(m) * N + n0 + nn] = swiglu_out<XT>(acc[0], acc[1]);
     }
@@ -458,27 +515,27 @@ __global__ __launch_bounds__(64 * S) void qmm_skinny_fac_kernel(QmmArgs a) {
 #pragma unroll
     for (int w2 = 0; w2 < S; ++w2)
 #pragma unroll
-      for (int g = 0; g < GB; ++g) acc += red[((w2 * NT + tt) * MT + i) * 256 + (mr + RPT * g) * 16 + (nn & 15)];
+      for (int g = 0; g < GR; ++g) acc += red[((w2 * NT + tt) * MT + i) * 256 + (mr + RPT * g) * 16 + (nn & 15)];
     if (n0 + nn < N) out[static_cast<int64_t>(m) * N + n0 + nn] = from_f<XT>(acc);
   }
 }
 
 namespace {
-template <int XT, int NT, int MT, int GB, bool GLU, int NB>
+template <int XT, int NT, int MT, int GB, bool GLU, int NB, bool TR>
 hipError_t fac_launch_nb(const QmmArgs& a, dim3 grid, int S) {
   switch (S) {
-    case 8: hipLaunchKernelGGL((qmm_skinny_fac_kernel<XT, NT, MT, GB, 8, NB, GLU>), grid, dim3(512), 0, a.stream, a); break;
-    case 4: hipLaunchKernelGGL((qmm_skinny_fac_kernel<XT, NT, MT, GB, 4, NB, GLU>), grid, dim3(256), 0, a.stream, a); break;
-    case 2: hipLaunchKernelGGL((qmm_skinny_fac_kernel<XT, NT, MT, GB, 2, NB, GLU>), grid, dim3(128), 0, a.stream, a); break;
-    default: hipLaunchKernelGGL((qmm_skinny_fac_kernel<XT, NT, MT, GB, 1, NB, GLU>), grid, dim3(64), 0, a.stream, a); break;
+    case 8: hipLaunchKernelGGL((qmm_skinny_fac_kernel<XT, NT, MT, GB, 8, NB, GLU, TR>), grid, dim3(512), 0, a.stream, a); break;
+    case 4: hipLaunchKernelGGL((qmm_skinny_fac_kernel<XT, NT, MT, GB, 4, NB, GLU, TR>), grid, dim3(256), 0, a.stream, a); break;
+    case 2: hipLaunchKernelGGL((qmm_skinny_fac_kernel<XT, NT, MT, GB, 2, NB, GLU, TR>), grid, dim3(128), 0, a.stream, a); break;
+    default: hipLaunchKernelGGL((qmm_skinny_fac_kernel<XT, NT, MT, GB, 1, NB, GLU, TR>), grid, dim3(64), 0, a.stream, a); break;
   }
   return hipGetLastError();
 }
-template <int XT, int NT, int MT, int GB, bool GLU>
+template <int XT, int NT, int MT, int GB, bool GLU, bool TR>
 hipError_t fac_launch_s(const QmmArgs& a, dim3 grid, int S) {
-  return fac_launch_nb<XT, NT, MT, GB, GLU, 2>(a, grid, S);
+  return fac_launch_nb<XT, NT, MT, GB, GLU, 2, TR>(a, grid, S);
 }
-template <int XT, int GB, bool GLU, int NT, int MT>
+template <int XT, int GB, bool GLU, int NT, int MT, bool TR = false>
 hipError_t fac_launch_gbn(const QmmArgs& a) {
   constexpr int NC = GLU ? 8 * NT : 16 * NT;  // output columns per workgroup
   const int64_t nwg = (a.N + NC - 1) / NC;
@@ -490,18 +547,28 @@ hipError_t fac_launch_gbn(const QmmArgs& a) {
   // the LDS partial tiles (S NT MT KiB) stay within 64 KiB so two workgroups fit a CU
   while (S > 1 && S * NT * MT > 64) S >>= 1;
   const dim3 grid(static_cast<unsigned>(nwg), static_cast<unsigned>(a.nbatch));
-  return fac_launch_s<XT, NT, MT, GB, GLU>(a, grid, S);
+  return fac_launch_s<XT, NT, MT, GB, GLU, TR>(a, grid, S);
 }
 template <int XT, int GB, bool GLU>
 hipError_t fac_launch_gb(const QmmArgs& a) {
-  // With two or more m tiles the x fragments (loaded per wave from L2) cost
-  // more than the weights; four weight tiles per wave halve the x loads per
-  // weight byte (measured 24.2 -> 21.4 us at M = 16, 35.6 -> 32.6 us at M = 32,
-  // N = 14336, K = 4096); with GLU, two gate and two up tiles.
-  constexpr int RPT = 16 / GB;
-  if (a.M <= RPT) return fac_launch_gbn<XT, GB, GLU, 2, 1>(a);
-  if (a.M <= 2 * RPT) return fac_launch_gbn<XT, GB, GLU, 4, 2>(a);
-  return fac_launch_gbn<XT, GB, GLU, 4, 4>(a);
+  // gs 32 / 64 (two or four groups per 128-code block): chunk-major k slots,
+  // every A row a live x row; four weight tiles per wave share each x
+  // fragment (measured at N = 14336, K = 4096, gs 64: M = 16 21.8 -> 20.5 us,
+  // M = 24 31.1 -> 23.0 us, M = 32 32.7 -> 24.1 us against the group-split
+  // rows; gs 32, M = 16: 30.1 -> 20.5 us).  Two tiles at gs 64 up to M = 8
+  // (M = 4: 17.8 against 18.7 us with four; gs 32 prefers four, 18.5 against
+  // 19.1 us) and for two m tiles at gs 32, whose four group accumulators would
+  // otherwise spill.
+  if constexpr (GB > 1) {
+    if (GB == 2 && a.M <= 8) return fac_launch_gbn<XT, GB, GLU, 2, 1, true>(a);
+    if (a.M <= 16) return fac_launch_gbn<XT, GB, GLU, 4, 1, true>(a);
+    if constexpr (GB == 4) return fac_launch_gbn<XT, GB, GLU, 2, 2, true>(a);
+    else return fac_launch_gbn<XT, GB, GLU, 4, 2, true>(a);
+  } else {
+    // gs 128: one group per block, so every A row is already live
+    if (a.M <= 16) return fac_launch_gbn<XT, GB, GLU, 2, 1>(a);
+    return fac_launch_gbn<XT, GB, GLU, 4, 2>(a);
+  }
 }
 template <int XT, bool GLU>
 hipError_t fac_launch(const QmmArgs& a) {
@@ -517,12 +584,11 @@ bool qmm_skinny_fac_supported(const QmmArgs& a) {
   if (!(a.transpose && a.mode == AFFINE && a.bits == 4 && (a.xdt == BF16 || a.xdt == F16) &&
         a.K % 128 == 0 && a.K >= 128))
     return false;
-  const int rpt = 16 / (128 / a.gs);   // x rows per m tile
   // with fewer than 2048 waves (8 per 32-row tile pair) the split-K skinny
   // kernel keeps more loads in flight
   // (GLU: 2N weight rows, 16 output columns per workgroup)
   const int64_t waves = (a.N + 31) / 32 * 8 * a.nbatch * (a.glu ? 2 : 1);
-  return a.M >= 1 && a.M <= 4 * rpt && a.M <= 32 && waves >= 2048;
+  return a.M >= 1 && a.M <= 32 && waves >= 2048;
 }
 
 hipError_t launch_qmm_skinny_fac(const QmmArgs& a) {

@@ -193,8 +193,8 @@ def test_qmm_split_k_tiles(ops, mode, bits, gs, M, xdt):
 @pytest.mark.parametrize("M", [4, 7, 8, 12, 16, 24, 32])
 def test_qmm_decode_widths_affine4(ops, M, gs, N, K, xdt):
     # decode batch widths of the 4-bit path.  N = 8200 (ragged 32-row tile)
-    # is wide enough for the factored MFMA kernel (M up to two m tiles of
-    # 16 * gs / 128 rows, K % 128 == 0; K = 1152 has an odd block count for
+    # is wide enough for the factored MFMA kernel (M up to two 16-row m
+    # tiles, K % 128 == 0; K = 1152 has an odd block count for
     # the split-K tail); N = 200 takes the split-K skinny kernel
     if N > 1000 and xdt == "f16" and M not in (8, 16):
         pytest.skip("f16 wide cases: M = 8, 16 cover the f16 magic constant")
