@@ -588,7 +588,10 @@ bool qmm_skinny_fac_supported(const QmmArgs& a) {
   // kernel keeps more loads in flight
   // (GLU: 2N weight rows, 16 output columns per workgroup)
   const int64_t waves = (a.N + 31) / 32 * 8 * a.nbatch * (a.glu ? 2 : 1);
-  return a.M >= 1 && a.M <= 32 && waves >= 2048;
+  // chunk-major slots load the 2 / 4 group scales and biases of a block as one
+  // 4- / 8-byte word
+  const bool aligned = (reinterpret_cast<uintptr_t>(a.s) | reinterpret_cast<uintptr_t>(a.b)) % 8 == 0;
+  return a.M >= 1 && a.M <= 32 && waves >= 2048 && (a.gs == 128 || aligned);
 }
 
 hipError_t launch_qmm_skinny_fac(const QmmArgs& a) {
@@ -627,10 +630,18 @@ __global__ __launch_bounds__(256) void segment_offsets_kernel(const void* rhs, i
 // before its first MFMA (CS x IT x 1 KiB of weights in flight per wave); each
 // x fragment (an L2-resident operand, loaded one group at a time) feeds the CS
 // strips' MFMAs.  The S partial tiles are summed through LDS.
-template <int XT, int MODE, int BITS, int IT, int CS>
+// GBT > 0 (affine 4-bit, GBT = 128 / gs groups per chunk group): chunk-major
+// k slots as in qmm_skinny_fac_kernel -- MFMA j of a chunk group takes chunk
+// 4p + j and lane (r, q) its 8-code piece q, so each x load is 64 contiguous
+// bytes per row; the weight dwords are transposed across the lanes q and each
+// dword j is dequantized with the scale / bias of chunk 4p + j.
+template <int XT, int MODE, int BITS, int IT, int CS, int GBT = 0>
 __global__ __launch_bounds__(512) void gather_sorted_kernel(QmmArgs a, int64_t nflat, const int64_t* off) {
   using XS = uint16_t;
   constexpr bool AFF = MODE == AFFINE;
+  constexpr bool TRX = GBT > 0;
+  static_assert(!TRX || (AFF && BITS == 4), "chunk-major slots: affine 4-bit");
+  using SG = typename std::conditional<GBT == 4, uint64_t, typename std::conditional<GBT == 2, uint32_t, XS>::type>::type;
   __shared__ float red[8][CS][16 * 17];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int S = blockDim.x >> 6;
@@ -673,6 +684,7 @@ __global__ __launch_bounds__(512) void gather_sorted_kernel(QmmArgs a, int64_t n
   // reused by every m tile
   uint32_t wd[CS][IT][BITS];
   float sv[CS][IT], bv[CS][IT], s2[CS][IT];
+  SG sg[TRX ? CS : 1][TRX ? IT : 1], bg[TRX ? CS : 1][TRX ? IT : 1];
 #pragma unroll
   for (int cs = 0; cs < CS; ++cs) {
     const int row = min(n0 + 16 * cs + nl, N - 1);
@@ -682,7 +694,13 @@ __global__ __launch_bounds__(512) void gather_sorted_kernel(QmmArgs a, int64_t n
       const int c = 4 * (p0 + it) + q;
       load_chunk<BITS>(wd[cs][it], wrow + c * BITS);
       const int gi = (c * 32) / gs;
-      if constexpr (AFF) {
+      if constexpr (TRX) {
+        // the GBT scales / biases of chunk group p0 + it, one load each
+        const int64_t g0 = static_cast<int64_t>(row) * G + (p0 + it) * GBT;
+        sg[cs][it] = *reinterpret_cast<const SG*>(sp + g0);
+        bg[cs][it] = *reinterpret_cast<const SG*>(bp + g0);
+        sv[cs][it] = bv[cs][it] = s2[cs][it] = 0.f;
+      } else if constexpr (AFF) {
         sv[cs][it] = to_f<XT>(sp[static_cast<int64_t>(row) * G + gi]);
         bv[cs][it] = to_f<XT>(bp[static_cast<int64_t>(row) * G + gi]);
         s2[cs][it] = sv[cs][it];
@@ -694,6 +712,21 @@ __global__ __launch_bounds__(512) void gather_sorted_kernel(QmmArgs a, int64_t n
     }
   }
 
+  if constexpr (TRX) {
+    // 4 x 4 dword transpose over the lanes q: wd[j] of lane q becomes dword q
+    // of chunk 4p + j (the chunk lane j loaded)
+#pragma unroll
+    for (int cs = 0; cs < CS; ++cs)
+#pragma unroll
+      for (int it = 0; it < IT; ++it) {
+        uint32_t (&v)[BITS] = wd[cs][it];
+        auto s02 = __builtin_amdgcn_permlane32_swap(v[0], v[2], false, false);
+        auto s13 = __builtin_amdgcn_permlane32_swap(v[1], v[3], false, false);
+        auto s01 = __builtin_amdgcn_permlane16_swap(s02[0], s13[0], false, false);
+        auto s23 = __builtin_amdgcn_permlane16_swap(s02[1], s13[1], false, false);
+        v[0] = s01[0]; v[1] = s01[1]; v[2] = s23[0]; v[3] = s23[1];
+      }
+  }
   for (int64_t r0 = 0; r0 < rows_total; r0 += 16) {
     // this lane's x row (A operand) of the 16-row tile
     const int64_t r = r0 + nl;
@@ -710,13 +743,33 @@ __global__ __launch_bounds__(512) void gather_sorted_kernel(QmmArgs a, int64_t n
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
       g_u32x4_t xa[4];
-      const g_u32x4_t* xp = reinterpret_cast<const g_u32x4_t*>(xrow + (4 * (p0 + it) + q) * 32);
+      if constexpr (TRX) {
+        // piece q of chunks 4 (p0 + it) + j
+        const XS* xg = xrow + 4 * (p0 + it) * 32 + 8 * q;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) xa[j] = xv ? xp[j] : g_u32x4_t{0, 0, 0, 0};
+        for (int j = 0; j < 4; ++j)
+          xa[j] = xv ? *reinterpret_cast<const g_u32x4_t*>(xg + 32 * j) : g_u32x4_t{0, 0, 0, 0};
+      } else {
+        const g_u32x4_t* xp = reinterpret_cast<const g_u32x4_t*>(xrow + (4 * (p0 + it) + q) * 32);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xa[j] = xv ? xp[j] : g_u32x4_t{0, 0, 0, 0};
+      }
 #pragma unroll
       for (int cs = 0; cs < CS; ++cs) {
         uint32_t o[16];
-        if constexpr (AFF && BITS == 4)
+        if constexpr (TRX) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int sh = 16 * ((j * GBT) >> 2);
+            const float s = to_f<XT>(static_cast<XS>(sg[cs][it] >> sh));
+            const float b = to_f<XT>(static_cast<XS>(bg[cs][it] >> sh));
+            const uint32_t lo = wd[cs][it][j] & 0x0F0F0F0Fu, hi = (wd[cs][it][j] >> 4) & 0x0F0F0F0Fu;
+            o[4 * j + 0] = pack2<XT>(fmaf(s, ubyte_f<0>(lo), b), fmaf(s, ubyte_f<0>(hi), b));
+            o[4 * j + 1] = pack2<XT>(fmaf(s, ubyte_f<1>(lo), b), fmaf(s, ubyte_f<1>(hi), b));
+            o[4 * j + 2] = pack2<XT>(fmaf(s, ubyte_f<2>(lo), b), fmaf(s, ubyte_f<2>(hi), b));
+            o[4 * j + 3] = pack2<XT>(fmaf(s, ubyte_f<3>(lo), b), fmaf(s, ubyte_f<3>(hi), b));
+          }
+        } else if constexpr (AFF && BITS == 4)
           deq4_fast<XT>(g_u32x4_t{wd[cs][it][0], wd[cs][it][1], wd[cs][it][2], wd[cs][it][3]}, sv[cs][it],
                         bv[cs][it], o);
         else
@@ -860,7 +913,7 @@ hipError_t skinny_by_mode(const QmmArgs& a) {
 }  // namespace
 
 namespace {
-template <int XT, int MODE, int BITS, int CS>
+template <int XT, int MODE, int BITS, int CS, int GBT = 0>
 hipError_t gather_launch_cs(const QmmArgs& a, int64_t nflat, int64_t E, const int64_t* off) {
   const int64_t ntiles = (a.N + 16 * CS - 1) / (16 * CS);
   if (ntiles > 0x7fffffffLL) return hipErrorInvalidConfiguration;
@@ -874,13 +927,13 @@ hipError_t gather_launch_cs(const QmmArgs& a, int64_t nflat, int64_t E, const in
   switch (it) {
     case 4:
       if constexpr (ITMAX >= 4)
-        hipLaunchKernelGGL((gather_sorted_kernel<XT, MODE, BITS, 4, CS>), grid, block, 0, a.stream, a, nflat, off);
+        hipLaunchKernelGGL((gather_sorted_kernel<XT, MODE, BITS, 4, CS, GBT>), grid, block, 0, a.stream, a, nflat, off);
       break;
     case 2:
       if constexpr (ITMAX >= 2)
-        hipLaunchKernelGGL((gather_sorted_kernel<XT, MODE, BITS, 2, CS>), grid, block, 0, a.stream, a, nflat, off);
+        hipLaunchKernelGGL((gather_sorted_kernel<XT, MODE, BITS, 2, CS, GBT>), grid, block, 0, a.stream, a, nflat, off);
       break;
-    case 1: hipLaunchKernelGGL((gather_sorted_kernel<XT, MODE, BITS, 1, CS>), grid, block, 0, a.stream, a, nflat, off); break;
+    case 1: hipLaunchKernelGGL((gather_sorted_kernel<XT, MODE, BITS, 1, CS, GBT>), grid, block, 0, a.stream, a, nflat, off); break;
     default: return hipErrorInvalidConfiguration;
   }
   return hipGetLastError();
@@ -891,6 +944,18 @@ hipError_t gather_launch_t(const QmmArgs& a, int64_t nflat, int64_t E, const int
   // four strips per wave: 4x the weight bytes in flight per wave and each x
   // fragment shared by four MFMAs (measured faster than one strip at 2 and
   // 16 rows per expert for both MoE projections)
+  // affine 4-bit: chunk-major k slots (measured at 256 experts, top 8, K =
+  // 2048: T = 512 gate 106.6 -> 85 us, T = 64 down 57.5 -> 56.2 us, others
+  // equal); the group scales / biases of a chunk group are one word
+  if constexpr (MODE == AFFINE && BITS == 4) {
+    if ((reinterpret_cast<uintptr_t>(a.s) | reinterpret_cast<uintptr_t>(a.b)) % 8 == 0) {
+      switch (a.gs) {
+        case 32: return gather_launch_cs<XT, MODE, BITS, 4, 4>(a, nflat, E, off);
+        case 64: return gather_launch_cs<XT, MODE, BITS, 4, 2>(a, nflat, E, off);
+        default: return gather_launch_cs<XT, MODE, BITS, 4, 1>(a, nflat, E, off);
+      }
+    }
+  }
   return gather_launch_cs<XT, MODE, BITS, 4>(a, nflat, E, off);
 }
 

@@ -452,3 +452,39 @@ def test_qmv_mxfp8_nan_code(ops):
     got = ops.quantized_matmul(from_np(x, "bf16"), words_to_torch(w), torch.from_numpy(s).cuda(), None, True,
                                mode="mxfp8").float().cpu().numpy()
     assert np.isnan(got[0, 5]) and not np.isnan(np.delete(got[0], 5)).any()
+
+
+def _misaligned(t):
+    """a copy of t whose data pointer is 2 bytes past an 8-byte boundary"""
+    flat = torch.empty(t.numel() + 1, dtype=t.dtype, device=t.device)[1:]
+    out = flat.view(t.shape)
+    out.copy_(t)
+    assert out.data_ptr() % 8 != 0
+    return out
+
+
+@pytest.mark.parametrize("gs", [32, 64])
+def test_decode_width_and_gather_misaligned_scales(ops, gs):
+    # the chunk-major decode-width and grouped-gather kernels read a block's
+    # group scales / biases as one 4- / 8-byte word; scale arrays that are not
+    # 8-byte aligned take the per-group kernels and give the same results
+    # within the matmul tolerance
+    rng = np.random.default_rng(gs)
+    N, K, M = 8200, 1152, 16
+    w, s, b = rand_affine(rng, N, K, gs, 4, "bf16")
+    tw, ts, tb = words_to_torch(w), from_np(s, "bf16"), from_np(b, "bf16")
+    x = from_np(oracle.from_float(rng.standard_normal((M, K)).astype(np.float32), "bf16"), "bf16")
+    got = ops.quantized_matmul(x, tw, _misaligned(ts), _misaligned(tb), True, gs, 4)
+    ref = ops.quantized_matmul(x, tw, ts, tb, True, gs, 4)
+    assert rel_err(as_f64(to_np(got, "bf16"), "bf16"), as_f64(to_np(ref, "bf16"), "bf16")) <= TOL["bf16"]
+    # grouped gather: 4 experts, 40 rows each
+    E, n, k2 = 4, 256, 1024
+    ws = [rand_affine(rng, n, k2, gs, 4, "bf16") for _ in range(E)]
+    tw2 = torch.stack([words_to_torch(u[0]) for u in ws])
+    ts2 = torch.stack([from_np(u[1], "bf16") for u in ws])
+    tb2 = torch.stack([from_np(u[2], "bf16") for u in ws])
+    xg = from_np(oracle.from_float(rng.standard_normal((E * 40, 1, k2)).astype(np.float32), "bf16"), "bf16")
+    rhs = torch.arange(E, device="cuda", dtype=torch.int32).repeat_interleave(40)
+    g1 = ops.gather_qmm(xg, tw2, _misaligned(ts2), _misaligned(tb2), None, rhs, True, gs, 4, "affine", True)
+    g0 = ops.gather_qmm(xg, tw2, ts2, tb2, None, rhs, True, gs, 4, "affine", True)
+    assert rel_err(as_f64(to_np(g1, "bf16"), "bf16"), as_f64(to_np(g0, "bf16"), "bf16")) <= TOL["bf16"]
