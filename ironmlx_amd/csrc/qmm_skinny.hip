@@ -559,9 +559,12 @@ hipError_t fac_launch_gb(const QmmArgs& a) {
   // (M = 4: 17.8 against 18.7 us with four; gs 32 prefers four, 18.5 against
   // 19.1 us) and for two m tiles at gs 32, whose four group accumulators would
   // otherwise spill.
+  const bool wide = static_cast<int64_t>(a.N) * a.nbatch * (a.glu ? 2 : 1) >= 8192;
   if constexpr (GB > 1) {
     if (GB == 2 && a.M <= 8) return fac_launch_gbn<XT, GB, GLU, 2, 1, true>(a);
-    if (a.M <= 16) return fac_launch_gbn<XT, GB, GLU, 4, 1, true>(a);
+    // four tiles halve the workgroups: only on matrices of >= 8192 rows
+    if (a.M <= 16 && wide) return fac_launch_gbn<XT, GB, GLU, 4, 1, true>(a);
+    if (a.M <= 16) return fac_launch_gbn<XT, GB, GLU, 2, 1, true>(a);
     if constexpr (GB == 4) return fac_launch_gbn<XT, GB, GLU, 2, 2, true>(a);
     else return fac_launch_gbn<XT, GB, GLU, 4, 2, true>(a);
   } else {
@@ -584,14 +587,15 @@ bool qmm_skinny_fac_supported(const QmmArgs& a) {
   if (!(a.transpose && a.mode == AFFINE && a.bits == 4 && (a.xdt == BF16 || a.xdt == F16) &&
         a.K % 128 == 0 && a.K >= 128))
     return false;
-  // with fewer than 2048 waves (8 per 32-row tile pair) the split-K skinny
-  // kernel keeps more loads in flight
+  // with fewer than 1536 waves (8 per 32-row tile pair) the split-K skinny
+  // kernel keeps more loads in flight (measured at K = 4096: N = 6144 runs
+  // faster here, 12.1 -> 10.1 us at M = 4, N = 4096 slower)
   // (GLU: 2N weight rows, 16 output columns per workgroup)
   const int64_t waves = (a.N + 31) / 32 * 8 * a.nbatch * (a.glu ? 2 : 1);
   // chunk-major slots load the 2 / 4 group scales and biases of a block as one
   // 4- / 8-byte word
   const bool aligned = (reinterpret_cast<uintptr_t>(a.s) | reinterpret_cast<uintptr_t>(a.b)) % 8 == 0;
-  return a.M >= 1 && a.M <= 32 && waves >= 2048 && (a.gs == 128 || aligned);
+  return a.M >= 1 && a.M <= 32 && waves >= 1536 && (a.gs == 128 || aligned);
 }
 
 hipError_t launch_qmm_skinny_fac(const QmmArgs& a) {

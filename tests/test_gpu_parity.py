@@ -188,7 +188,7 @@ def test_qmm_split_k_tiles(ops, mode, bits, gs, M, xdt):
 
 
 @pytest.mark.parametrize("xdt", ["bf16", "f16"])
-@pytest.mark.parametrize("N,K", [(200, 512), (8200, 1152)])
+@pytest.mark.parametrize("N,K", [(200, 512), (6144, 1024), (8200, 1152)])
 @pytest.mark.parametrize("gs", [32, 64, 128])
 @pytest.mark.parametrize("M", [4, 7, 8, 12, 16, 24, 32])
 def test_qmm_decode_widths_affine4(ops, M, gs, N, K, xdt):
