@@ -465,18 +465,19 @@ def _misaligned(t):
 
 @pytest.mark.parametrize("gs", [32, 64])
 def test_decode_width_and_gather_misaligned_scales(ops, gs):
-    # the chunk-major decode-width and grouped-gather kernels read a block's
+    # the chunk-major decode-width, skinny and grouped-gather kernels read a block's
     # group scales / biases as one 4- / 8-byte word; scale arrays that are not
     # 8-byte aligned take the per-group kernels and give the same results
     # within the matmul tolerance
     rng = np.random.default_rng(gs)
-    N, K, M = 8200, 1152, 16
-    w, s, b = rand_affine(rng, N, K, gs, 4, "bf16")
-    tw, ts, tb = words_to_torch(w), from_np(s, "bf16"), from_np(b, "bf16")
-    x = from_np(oracle.from_float(rng.standard_normal((M, K)).astype(np.float32), "bf16"), "bf16")
-    got = ops.quantized_matmul(x, tw, _misaligned(ts), _misaligned(tb), True, gs, 4)
-    ref = ops.quantized_matmul(x, tw, ts, tb, True, gs, 4)
-    assert rel_err(as_f64(to_np(got, "bf16"), "bf16"), as_f64(to_np(ref, "bf16"), "bf16")) <= TOL["bf16"]
+    # factored kernel (8200 rows) and split-K skinny kernel (200 rows)
+    for N, K, M in ((8200, 1152, 16), (200, 512, 8)):
+        w, s, b = rand_affine(rng, N, K, gs, 4, "bf16")
+        tw, ts, tb = words_to_torch(w), from_np(s, "bf16"), from_np(b, "bf16")
+        x = from_np(oracle.from_float(rng.standard_normal((M, K)).astype(np.float32), "bf16"), "bf16")
+        got = ops.quantized_matmul(x, tw, _misaligned(ts), _misaligned(tb), True, gs, 4)
+        ref = ops.quantized_matmul(x, tw, ts, tb, True, gs, 4)
+        assert rel_err(as_f64(to_np(got, "bf16"), "bf16"), as_f64(to_np(ref, "bf16"), "bf16")) <= TOL["bf16"]
     # grouped gather: 4 experts, 40 rows each
     E, n, k2 = 4, 256, 1024
     ws = [rand_affine(rng, n, k2, gs, 4, "bf16") for _ in range(E)]
