@@ -603,7 +603,10 @@ hipError_t fac_launch_gb(const QmmArgs& a) {
     // four tiles halve the workgroups: only on matrices of >= 8192 rows
     if (a.M <= 16 && wide) return fac_launch_gbn<XT, GB, GLU, 4, 1, true>(a);
     if (a.M <= 16) return fac_launch_gbn<XT, GB, GLU, 2, 1, true>(a);
+    // two m tiles: two weight tiles below 8192 rows (N = 6144, M = 32: 22.7 ->
+    // 16.4 us), four from 8192 (N = 14336, M = 32: 31.2 -> 24.4 us)
     if constexpr (GB == 4) return fac_launch_gbn<XT, GB, GLU, 2, 2, true>(a);
+    else if (!wide) return fac_launch_gbn<XT, GB, GLU, 2, 2, true>(a);
     else return fac_launch_gbn<XT, GB, GLU, 4, 2, true>(a);
   } else {
     // gs 128: one group per block, so every A row is already live
