@@ -244,6 +244,23 @@ def graph_time(fn, n):
     return t0.elapsed_time(t1) * 1e-3 / n
 
 
+def bench_decode_widths(ops, shapes=((14336, 4096), (6144, 4096), (4096, 14336), (4096, 4096)),
+                        Ms=(2, 4, 8, 16, 24, 32), steps=10, warmup=2):
+    """Decode batch widths of the 4-bit gs64 path on the Llama-3-8B projection
+    shapes (gate/up, fused q/k/v, down, o): per-launch time over a rotating
+    weight pool (graph replay, as the M = 1 headline), weight GB/s and
+    TFLOP/s."""
+    out = {}
+    for N, K in shapes:
+        row = {}
+        for M in Ms:
+            r = bench_gemv(ops, steps, warmup, M=M, N=N, K=K)
+            row[str(M)] = {"us": round(r["avg_launch_us"], 2), "gbs": round(r["kernel_gbs"], 1),
+                           "tflops": round(2.0 * M * N * K / (r["avg_launch_us"] * 1e-6) / 1e12, 1)}
+        out[f"N{N}_K{K}"] = row
+    return out
+
+
 def bench_mode_sweep(ops, K=4096, N=4096, Ms=(1, 256), n=20):
     """Mode / bit-width sweep at K = N = 4096: weights ~N(0, 0.02) quantized by
     the library's own quantize for each mode, bf16 x; M = 1 reports weight GB/s,
@@ -526,6 +543,8 @@ def run_only(ops, args):
         return {"only": "fused", **bench_fused(ops)}
     if args.only == "llama":
         return {"only": "llama", **bench_llama_decode(ops)}
+    if args.only == "widths":
+        return {"only": "widths", **bench_decode_widths(ops)}
     nbytes = 256 << 20
     a = torch.empty(nbytes // 4, dtype=torch.int32, device="cuda").fill_(1)
     b = torch.empty_like(a)
@@ -553,8 +572,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-llama", action="store_true")
     ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-widths", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--only", choices=["gemv", "prefill", "moe", "sweep", "fused", "llama", "copy"], default=None,
+    ap.add_argument("--only", choices=["gemv", "prefill", "moe", "sweep", "fused", "llama", "widths", "copy"], default=None,
                     help="run one workload (for rocprofv3 kernel-trace / counter passes)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -575,6 +595,7 @@ def main():
     prefill_down = bench_prefill(ops, args.steps, args.warmup, N=4096, K=14336)
     moe = bench_moe(ops)
     sweep = None if args.no_sweep else bench_mode_sweep(ops)
+    widths = None if args.no_widths else bench_decode_widths(ops)
     llama = None if args.no_llama else bench_llama_decode(ops)
     fused = bench_fused(ops)
     tr = load_traffic()
@@ -618,6 +639,8 @@ def main():
     }
     if sweep is not None:
         line["mode_sweep_k4096_n4096"] = sweep
+    if widths is not None:
+        line["decode_widths_q4_gs64"] = widths
     if llama is not None:
         line["llama3_8b_decode"] = llama
     if not args.no_cpu:
