@@ -81,7 +81,7 @@ hipError_t launch_moe_combine(const void* y, int dt, const int32_t* inverse, con
 // Scratch of one call: the (device, stream, slot) buffer when it is large
 // enough (or can grow: not during capture), else a fresh hipMallocAsync block
 // with *owned = true that the caller releases with hipFreeAsync on `st`.
-enum WsSlot : int { WS_SPLITK = 0, WS_GLU = 1, WS_OFFSETS = 2 };
+enum WsSlot : int { WS_SPLITK = 0, WS_GLU = 1, WS_OFFSETS = 2, WS_SORT = 3 };
 hipError_t workspace_get(hipStream_t st, int slot, size_t bytes, void** p, bool* owned);
 
 }  // namespace iqmm

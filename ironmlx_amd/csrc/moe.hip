@@ -155,6 +155,83 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(const int32_t* experts, 
   }
 }
 
+// Stable counting sort over blocks of 256 rows (bucket = expert for ids in
+// [0, E), E otherwise), the same order as the key sort above.
+// moe_count_kernel: per-block bucket counts, stored expert-major
+// hist[bucket * nb + block].  moe_scatter_kernel: every block scans the whole
+// histogram in LDS (an exclusive prefix in expert-major order gives the first
+// position of each (bucket, block)), ranks its rows among the earlier rows of
+// the block with the same bucket, and writes them; block 0 writes the offsets.
+constexpr int SORT_BLOCK = 256;
+
+__global__ __launch_bounds__(SORT_BLOCK) void moe_count_kernel(const int32_t* experts, int n, int E, int nb,
+                                                               int32_t* hist) {
+  extern __shared__ int32_t h[];  // E + 1 counts
+  const int tid = threadIdx.x;
+  for (int e = tid; e <= E; e += SORT_BLOCK) h[e] = 0;
+  __syncthreads();
+  const int i = blockIdx.x * SORT_BLOCK + tid;
+  if (i < n) {
+    const int e = experts[i];
+    atomicAdd(&h[(e >= 0 && e < E) ? e : E], 1);
+  }
+  __syncthreads();
+  for (int e = tid; e <= E; e += SORT_BLOCK) hist[static_cast<int64_t>(e) * nb + blockIdx.x] = h[e];
+}
+
+__global__ __launch_bounds__(SORT_BLOCK) void moe_scatter_kernel(const int32_t* experts, int n, int k, int E, int nb,
+                                                                 const int32_t* hist, int32_t* tokens, int32_t* sorted,
+                                                                 int32_t* inverse, int32_t* offsets) {
+  extern __shared__ int32_t s[];  // L prefix entries, SORT_BLOCK partials, SORT_BLOCK buckets
+  const int L = (E + 1) * nb;
+  int32_t* part = s + L;
+  int32_t* kb = part + SORT_BLOCK;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int j = tid; j < L; j += SORT_BLOCK) s[j] = hist[j];
+  const int i = blockIdx.x * SORT_BLOCK + tid;
+  int bucket = -1;
+  if (i < n) {
+    const int e = experts[i];
+    bucket = (e >= 0 && e < E) ? e : E;
+  }
+  kb[tid] = bucket;
+  __syncthreads();
+  // exclusive prefix of s: each thread a contiguous segment, then the segment sums
+  const int per = (L + SORT_BLOCK - 1) / SORT_BLOCK;
+  const int lo = min(tid * per, L), hi = min(lo + per, L);
+  int sum = 0;
+  for (int j = lo; j < hi; ++j) {
+    const int v = s[j];
+    s[j] = sum;
+    sum += v;
+  }
+  // inclusive scan of the segment sums: within each wave, then across waves
+  int inc = sum;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int o = __shfl_up(inc, off, 64);
+    if (lane >= off) inc += o;
+  }
+  if (lane == 63) part[wave] = inc;
+  __syncthreads();
+  int base = 0;
+  for (int w = 0; w < wave; ++w) base += part[w];
+  const int add = base + inc - sum;  // exclusive prefix of this segment
+  for (int j = lo; j < hi; ++j) s[j] += add;
+  // stable rank among the earlier rows of this block with the same bucket
+  int rank = 0;
+  for (int j = 0; j < tid; ++j) rank += kb[j] == bucket ? 1 : 0;
+  __syncthreads();
+  if (i < n) {
+    const int pos = s[bucket * nb + blockIdx.x] + rank;
+    tokens[pos] = i / k;
+    sorted[pos] = experts[i];
+    inverse[i] = pos;
+  }
+  if (blockIdx.x == 0 && offsets != nullptr)
+    for (int e = tid; e <= E; e += SORT_BLOCK) offsets[e] = s[e * nb];
+}
+
 // out[t, d] = sum over t's valid slots in ascending expert order of
 // float(y[pos, d]) * score.  One workgroup per token: the k slots are ranked
 // once (in LDS), then each thread runs the ordered sum for its column
@@ -249,6 +326,28 @@ hipError_t launch_moe_route(const void* logits, int dt, float* scores, int32_t* 
 
 hipError_t launch_moe_sort(const int32_t* experts, int n, int k, int E, int32_t* tokens, int32_t* sorted,
                            int32_t* inverse, int32_t* offsets, hipStream_t st) {
+  // counting sort when the (bucket, block) histogram fits one workgroup's LDS
+  // with its partials: 64 KiB
+  const int nb = (n + SORT_BLOCK - 1) / SORT_BLOCK;
+  const int64_t L = (static_cast<int64_t>(E) + 1) * nb;
+  if (n > 0 && L + 2 * SORT_BLOCK <= 16384) {
+    void* ws = nullptr;
+    bool owned = false;
+    hipError_t e = workspace_get(st, WS_SORT, static_cast<size_t>(L) * 4, &ws, &owned);
+    if (e != hipSuccess) return e;
+    int32_t* hist = static_cast<int32_t*>(ws);
+    hipLaunchKernelGGL(moe_count_kernel, dim3(nb), dim3(SORT_BLOCK), static_cast<size_t>(E + 1) * 4, st, experts, n,
+                       E, nb, hist);
+    e = hipGetLastError();
+    if (e == hipSuccess) {
+      hipLaunchKernelGGL(moe_scatter_kernel, dim3(nb), dim3(SORT_BLOCK),
+                         static_cast<size_t>(L + 2 * SORT_BLOCK) * 4, st, experts, n, k, E, nb, hist, tokens, sorted,
+                         inverse, offsets);
+      e = hipGetLastError();
+    }
+    const hipError_t f = owned ? hipFreeAsync(ws, st) : hipSuccess;
+    return e != hipSuccess ? e : f;
+  }
   int np = 2;
   while (np < n) np <<= 1;
   const size_t lds = static_cast<size_t>(np) * 4;
