@@ -455,7 +455,14 @@ int gather_entry(const char* op, iqmm_array* res, iqmm_array x, iqmm_array w, iq
   const bool grouped = sorted_indices && one_to_one && nwm + 1 <= 65535 && gather_sorted_supported(a) &&
                        !(gemv_ok && rows_per_expert <= 4);
   auto product = [&](QmmArgs& p) { return grouped ? launch_gather_sorted(p, p.nbatch, nwm) : run_qmm(p); };
-  hipError_t e = glu ? run_glu(a, !grouped, product) : product(a);
+  hipError_t e;
+  if (glu && grouped && gather_sorted_glu_supported(a)) {
+    // SwiGLU in the grouped kernel's epilogue
+    a.glu = 1;
+    e = launch_gather_sorted(a, a.nbatch, nwm);
+  } else {
+    e = glu ? run_glu(a, !grouped, product) : product(a);
+  }
   return e == hipSuccess ? 0 : hip_fail(op, e);
 }
 }  // namespace

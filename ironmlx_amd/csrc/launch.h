@@ -64,6 +64,8 @@ bool qmm_skinny_fac_supported(const QmmArgs& a);
 // sorted-expert grouped gather_qmm: nflat batch elements, E experts
 hipError_t launch_gather_sorted(const QmmArgs& a, int64_t nflat, int64_t E);
 bool gather_sorted_supported(const QmmArgs& a);
+// with glu: the weight holds 2N rows per expert, out[., n] = silu(gate_n) * up_n
+bool gather_sorted_glu_supported(const QmmArgs& a);
 bool qmm_gemm_supported(const QmmArgs& a);
 hipError_t launch_dequantize(const ConvArgs& a);
 hipError_t launch_quantize(const ConvArgs& a);

@@ -680,7 +680,10 @@ __global__ __launch_bounds__(256) void segment_offsets_kernel(const void* rhs, i
 // 4p + j and lane (r, q) its 8-code piece q, so each x load is 64 contiguous
 // bytes per row; the weight dwords are transposed across the lanes q and each
 // dword j is dequantized with the scale / bias of chunk 4p + j.
-template <int XT, int MODE, int BITS, int IT, int CS, int GBT = 0>
+// GLU (CS even): each expert holds 2N rows (gate [0, N), up [N, 2N)); strips
+// [0, CS/2) are gate columns n0.. and [CS/2, CS) the matching up columns, and
+// the epilogue writes silu(gate) * up for 8 CS columns.
+template <int XT, int MODE, int BITS, int IT, int CS, int GBT = 0, bool GLU = false>
 __global__ __launch_bounds__(512) void gather_sorted_kernel(QmmArgs a, int64_t nflat, const int64_t* off) {
   using XS = uint16_t;
   constexpr bool AFF = MODE == AFFINE;
@@ -691,7 +694,9 @@ __global__ __launch_bounds__(512) void gather_sorted_kernel(QmmArgs a, int64_t n
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int S = blockDim.x >> 6;
   const int Mx = a.M, N = a.N, K = a.K;
-  const int n0 = blockIdx.x * 16 * CS;
+  static_assert(!GLU || CS % 2 == 0, "GLU pairs gate strips with up strips");
+  constexpr int NC = GLU ? 8 * CS : 16 * CS;  // output columns per workgroup
+  const int n0 = blockIdx.x * NC;
   const int64_t e = blockIdx.y;
   if (e == a.bm.nw) {
     // offsets are clamped into [0, nflat]: indices that are not sorted as
@@ -700,7 +705,6 @@ __global__ __launch_bounds__(512) void gather_sorted_kernel(QmmArgs a, int64_t n
     const int64_t end_valid = min(max(off[e], first_valid), nflat);
     XS* o = static_cast<XS*>(a.out);
     const int64_t nbad = first_valid + (nflat - end_valid);
-    constexpr int NC = 16 * CS;
     for (int64_t i = t; i < nbad * Mx * NC; i += blockDim.x) {
       const int64_t rr = i / NC, n = i % NC;
       const int64_t bi = rr / Mx, mrow = rr % Mx;
@@ -732,7 +736,8 @@ __global__ __launch_bounds__(512) void gather_sorted_kernel(QmmArgs a, int64_t n
   SG sg[TRX ? CS : 1][TRX ? IT : 1], bg[TRX ? CS : 1][TRX ? IT : 1];
 #pragma unroll
   for (int cs = 0; cs < CS; ++cs) {
-    const int row = min(n0 + 16 * cs + nl, N - 1);
+    const int row = GLU ? (cs / (CS / 2)) * N + min(n0 + 16 * (cs % (CS / 2)) + nl, N - 1)
+                        : min(n0 + 16 * cs + nl, N - 1);
     const uint32_t* wrow = w + static_cast<int64_t>(row) * wpr;
 #pragma unroll
     for (int it = 0; it < IT; ++it) {
@@ -830,6 +835,24 @@ __global__ __launch_bounds__(512) void gather_sorted_kernel(QmmArgs a, int64_t n
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) red[wave][cs][(4 * q + rr) * 17 + nl] = acc[cs][rr];
     __syncthreads();
+    if constexpr (GLU) {
+      for (int i = t; i < (CS / 2) * 16 * 16; i += blockDim.x) {
+        const int cs = i / 256, m = (i / 16) % 16, n = i % 16;
+        const int64_t rm = r0 + m;
+        const int col = n0 + 16 * cs + n;
+        if (rm < rows_total && col < N) {
+          float g = 0.f, u = 0.f;
+          for (int w2 = 0; w2 < S; ++w2) g += red[w2][cs][m * 17 + n];
+          for (int w2 = 0; w2 < S; ++w2) u += red[w2][cs + CS / 2][m * 17 + n];
+          const int64_t bb = blo + rm / Mx, mr = rm % Mx;
+          const int64_t xi = a.bm.lhs ? load_index(a.bm.lhs, a.bm.lhs_dt, bb) : bb;
+          const bool ok = xi >= 0 && xi < a.bm.nx;
+          out[(bb * Mx + mr) * N + col] = ok ? swiglu_out<XT>(g, u) : from_f<XT>(__builtin_nanf(""));
+        }
+      }
+      __syncthreads();
+      continue;
+    }
     for (int i = t; i < CS * 16 * 16; i += blockDim.x) {
       const int cs = i / 256, m = (i / 16) % 16, n = i % 16;
       const int64_t rm = r0 + m;
@@ -858,6 +881,12 @@ int gather_groups_per_wave(int K, int itmax) {
   for (int it = itmax; it >= 1; it >>= 1)
     if (P % it == 0 && P / it <= 8) return it;
   return 0;
+}
+
+// the SwiGLU epilogue: affine 4-bit with 8-byte aligned scales / biases
+bool gather_sorted_glu_supported(const QmmArgs& a) {
+  return a.mode == AFFINE && a.bits == 4 &&
+         (reinterpret_cast<uintptr_t>(a.s) | reinterpret_cast<uintptr_t>(a.b)) % 8 == 0;
 }
 
 bool gather_sorted_supported(const QmmArgs& a) {
@@ -976,9 +1005,10 @@ hipError_t skinny_by_mode(const QmmArgs& a) {
 }  // namespace
 
 namespace {
-template <int XT, int MODE, int BITS, int CS, int GBT = 0>
+template <int XT, int MODE, int BITS, int CS, int GBT = 0, bool GLU = false>
 hipError_t gather_launch_cs(const QmmArgs& a, int64_t nflat, int64_t E, const int64_t* off) {
-  const int64_t ntiles = (a.N + 16 * CS - 1) / (16 * CS);
+  constexpr int NC = GLU ? 8 * CS : 16 * CS;
+  const int64_t ntiles = (a.N + NC - 1) / NC;
   if (ntiles > 0x7fffffffLL) return hipErrorInvalidConfiguration;
   const dim3 grid(static_cast<unsigned>(ntiles), static_cast<unsigned>(E + 1));
   // IT chunk groups (128 k each, P = K / 128) per wave, P / IT <= 8 waves.
@@ -990,13 +1020,13 @@ hipError_t gather_launch_cs(const QmmArgs& a, int64_t nflat, int64_t E, const in
   switch (it) {
     case 4:
       if constexpr (ITMAX >= 4)
-        hipLaunchKernelGGL((gather_sorted_kernel<XT, MODE, BITS, 4, CS, GBT>), grid, block, 0, a.stream, a, nflat, off);
+        hipLaunchKernelGGL((gather_sorted_kernel<XT, MODE, BITS, 4, CS, GBT, GLU>), grid, block, 0, a.stream, a, nflat, off);
       break;
     case 2:
       if constexpr (ITMAX >= 2)
-        hipLaunchKernelGGL((gather_sorted_kernel<XT, MODE, BITS, 2, CS, GBT>), grid, block, 0, a.stream, a, nflat, off);
+        hipLaunchKernelGGL((gather_sorted_kernel<XT, MODE, BITS, 2, CS, GBT, GLU>), grid, block, 0, a.stream, a, nflat, off);
       break;
-    case 1: hipLaunchKernelGGL((gather_sorted_kernel<XT, MODE, BITS, 1, CS, GBT>), grid, block, 0, a.stream, a, nflat, off); break;
+    case 1: hipLaunchKernelGGL((gather_sorted_kernel<XT, MODE, BITS, 1, CS, GBT, GLU>), grid, block, 0, a.stream, a, nflat, off); break;
     default: return hipErrorInvalidConfiguration;
   }
   return hipGetLastError();
@@ -1012,6 +1042,13 @@ hipError_t gather_launch_t(const QmmArgs& a, int64_t nflat, int64_t E, const int
   // equal); the group scales / biases of a chunk group are one word
   if constexpr (MODE == AFFINE && BITS == 4) {
     if ((reinterpret_cast<uintptr_t>(a.s) | reinterpret_cast<uintptr_t>(a.b)) % 8 == 0) {
+      if (a.glu) {
+        switch (a.gs) {
+          case 32: return gather_launch_cs<XT, MODE, BITS, 4, 4, true>(a, nflat, E, off);
+          case 64: return gather_launch_cs<XT, MODE, BITS, 4, 2, true>(a, nflat, E, off);
+          default: return gather_launch_cs<XT, MODE, BITS, 4, 1, true>(a, nflat, E, off);
+        }
+      }
       switch (a.gs) {
         case 32: return gather_launch_cs<XT, MODE, BITS, 4, 4>(a, nflat, E, off);
         case 64: return gather_launch_cs<XT, MODE, BITS, 4, 2>(a, nflat, E, off);
@@ -1019,6 +1056,7 @@ hipError_t gather_launch_t(const QmmArgs& a, int64_t nflat, int64_t E, const int
       }
     }
   }
+  if (a.glu) return hipErrorInvalidValue;  // callers check gather_sorted_glu_supported
   return gather_launch_cs<XT, MODE, BITS, 4>(a, nflat, E, off);
 }
 
