@@ -452,8 +452,12 @@ int gather_entry(const char* op, iqmm_array* res, iqmm_array x, iqmm_array w, iq
   QmmArgs probe = a;
   probe.N = glu ? 2 * a.N : a.N;
   const bool gemv_ok = qmv_q4_m1_supported(probe);
+  // The grouped kernel's SwiGLU epilogue (affine 4-bit) is faster than the
+  // per-row fused GEMV from 512 rows on (T = 64 of a 256-expert top-8 expert
+  // block: 189 against 194 us).
+  const bool glu_grouped = glu && a.nbatch * a.M >= 512 && gather_sorted_glu_supported(a);
   const bool grouped = sorted_indices && one_to_one && nwm + 1 <= 65535 && gather_sorted_supported(a) &&
-                       !(gemv_ok && rows_per_expert <= 4);
+                       (glu_grouped || !(gemv_ok && rows_per_expert <= 4));
   auto product = [&](QmmArgs& p) { return grouped ? launch_gather_sorted(p, p.nbatch, nwm) : run_qmm(p); };
   hipError_t e;
   if (glu && grouped && gather_sorted_glu_supported(a)) {
