@@ -22,8 +22,51 @@ namespace iqmm {
 
 namespace {
 
+// Value of the partner lane in step `st` of an all-reduce over the wave:
+// quad xor 1, quad xor 2 (DPP quad_perm), 7 - i within 8 (row_half_mirror),
+// 15 - i within 16 (row_mirror), the other row of a 32-lane half
+// (v_permlane16_swap) and the other half (v_permlane32_swap).  Every step
+// pairs lanes symmetrically, so an order-independent reduction (max, argmax
+// on distinct keys) leaves the same result in every lane; no LDS traffic.
+template <int ST>
+__device__ __forceinline__ uint32_t wave_partner(uint32_t x) {
+  if constexpr (ST == 0) return __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false);
+  else if constexpr (ST == 1) return __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false);
+  else if constexpr (ST == 2) return __builtin_amdgcn_mov_dpp(x, 0x141, 0xF, 0xF, false);
+  else if constexpr (ST == 3) return __builtin_amdgcn_mov_dpp(x, 0x140, 0xF, 0xF, false);
+  else if constexpr (ST == 4) {
+    const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    return ((threadIdx.x >> 4) & 1) ? r[0] : r[1];
+  } else {
+    const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return ((threadIdx.x >> 5) & 1) ? r[0] : r[1];
+  }
+}
+
+template <int ST>
+__device__ __forceinline__ void argmax_step(float& bv, int& bi) {
+  const float ov = __uint_as_float(wave_partner<ST>(__float_as_uint(bv)));
+  const int oi = static_cast<int>(wave_partner<ST>(static_cast<uint32_t>(bi)));
+  if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+}
+
+// wave-wide (largest value, then lowest index), identical in every lane
+__device__ __forceinline__ void wave_argmax(float& bv, int& bi) {
+  argmax_step<0>(bv, bi);
+  argmax_step<1>(bv, bi);
+  argmax_step<2>(bv, bi);
+  argmax_step<3>(bv, bi);
+  argmax_step<4>(bv, bi);
+  argmax_step<5>(bv, bi);
+}
+
 __device__ __forceinline__ float wave_max(float v) {
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  v = fmaxf(v, __uint_as_float(wave_partner<0>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(wave_partner<1>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(wave_partner<2>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(wave_partner<3>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(wave_partner<4>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(wave_partner<5>(__float_as_uint(v))));
   return v;
 }
 
@@ -75,11 +118,7 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const typename Store<DT>
       const int e = lane + 64 * j;
       if (p[j] > bv) { bv = p[j]; bi = e; }  // ascending e within a lane: ties keep the first
     }
-    for (int off = 32; off > 0; off >>= 1) {
-      const float ov = __shfl_xor(bv, off, 64);
-      const int oi = __shfl_xor(bi, off, 64);
-      if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-    }
+    wave_argmax(bv, bi);
     if ((bi & 63) == lane) {
 #pragma unroll
       for (int j = 0; j < PL; ++j)
