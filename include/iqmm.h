@@ -43,21 +43,23 @@
  * Scratch memory: the fp32 partial sums of a split-K GEMM (few output tiles,
  * M > 64), the gate_up product of a fused SwiGLU outside its fused kernels,
  * the expert segment offsets of a sorted grouped gather_qmm and the per-block
- * bucket counts of iqmm_moe_sort live in per-stream
- * workspaces: one grow-only buffer per (device, stream, use), taken from the
- * stream-ordered pool (hipMallocAsync on `stream`) and kept until the process
- * ends, so HIP graphs captured on a stream keep valid pointers and need no
- * allocation nodes.  A capture on a stream whose buffer is too small (no
- * eager call on that stream yet) falls back to a hipMallocAsync /
- * hipFreeAsync pair inside the graph.  Calls are re-entrant across streams;
- * calls on one stream execute in order and share its workspaces, so a graph
- * must not be replayed concurrently with other library work on the stream it
- * was captured on.
+ * bucket counts of iqmm_moe_sort live in per-stream workspaces: one
+ * grow-only buffer per (device, stream, use), taken from the stream-ordered
+ * pool (hipMallocAsync on `stream`) and kept until the process ends, so HIP
+ * graphs captured on a stream keep valid pointers and hold kernel nodes only.
+ * Nothing is allocated while `stream` is capturing: a call whose workspace
+ * would have to grow then fails with a message saying so.  Size the
+ * workspaces before capture by running the same calls once on the capture
+ * stream, or with iqmm_workspace_reserve.  Calls are re-entrant across
+ * streams; calls on one stream execute in order and share its workspaces, so
+ * a graph must not be replayed concurrently with other library work on the
+ * stream it was captured on, nor with another graph captured on that stream.
  */
 #ifndef IQMM_H
 #define IQMM_H
 
 #include <stdbool.h>
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -243,6 +245,14 @@ int iqmm_moe_combine(iqmm_array* res, iqmm_array y, iqmm_array inverse, iqmm_arr
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* iqmm_last_error(void);
+
+/*
+ * Grow every workspace of `stream` (on the current device) to at least
+ * `bytes`, outside graph capture, so that later captured calls on that stream
+ * need no allocation.  No counterpart in mlx-c (MLX allocates per array); it
+ * is for callers that capture the library's calls into HIP graphs.
+ */
+int iqmm_workspace_reserve(iqmm_stream stream, size_t bytes);
 
 /* Library version string, e.g. "iqmm 0.1 gfx950". */
 const char* iqmm_version(void);

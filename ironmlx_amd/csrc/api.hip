@@ -32,6 +32,10 @@ int fail(const char* fmt, ...) {
 }
 
 int hip_fail(const char* op, hipError_t e) {
+  if (e == hipErrorStreamCaptureUnsupported)
+    return fail("[%s] the stream's workspace is too small for this call during graph capture (nothing is "
+                "allocated while capturing): run the same call once on this stream before capturing, or "
+                "call iqmm_workspace_reserve on it.", op);
   return fail("[%s] HIP error: %s", op, hipGetErrorString(e));
 }
 
@@ -225,17 +229,15 @@ hipError_t run_glu(QmmArgs& a, bool try_fused, F&& product) {
   const int64_t I = a.N, rows = a.nbatch * a.M;
   void* out = a.out;
   void* ws = nullptr;
-  bool owned = false;
-  hipError_t e = workspace_get(a.stream, WS_GLU, static_cast<size_t>(rows) * 2 * I * elt_size(a.xdt), &ws, &owned);
+  hipError_t e = workspace_get(a.stream, WS_GLU, static_cast<size_t>(rows) * 2 * I * elt_size(a.xdt), &ws);
   if (e != hipSuccess) return e;
   a.N = static_cast<int>(2 * I);
   a.out = ws;
   e = product(a);
   if (e == hipSuccess) e = launch_swiglu_rows(ws, out, rows, I, a.xdt, a.stream);
-  const hipError_t f = owned ? hipFreeAsync(ws, a.stream) : hipSuccess;
   a.N = static_cast<int>(I);
   a.out = out;
-  return e != hipSuccess ? e : f;
+  return e;
 }
 
 // common core of quantized_matmul / gather_qmm once batch mapping is known
@@ -286,6 +288,16 @@ extern "C" {
 const char* iqmm_last_error(void) { return g_last_error.c_str(); }
 
 const char* iqmm_version(void) { return "iqmm 0.1 gfx950"; }
+
+int iqmm_workspace_reserve(iqmm_stream stream, size_t bytes) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  hipError_t e = hipStreamIsCapturing(static_cast<hipStream_t>(stream), &cs);
+  if (e != hipSuccess) return hip_fail("workspace_reserve", e);
+  if (cs != hipStreamCaptureStatusNone)
+    return fail("[workspace_reserve] the stream is capturing; reserve before capture.");
+  e = workspace_reserve(static_cast<hipStream_t>(stream), bytes);
+  return e != hipSuccess ? hip_fail("workspace_reserve", e) : 0;
+}
 
 }  // extern "C"
 

@@ -80,10 +80,12 @@ hipError_t launch_moe_sort(const int32_t* experts, int n, int k, int E, int32_t*
 hipError_t launch_moe_combine(const void* y, int dt, const int32_t* inverse, const int32_t* experts,
                               const float* scores, float* out, int T, int k, int64_t D, int E, int64_t n,
                               hipStream_t st);
-// Scratch of one call: the (device, stream, slot) buffer when it is large
-// enough (or can grow: not during capture), else a fresh hipMallocAsync block
-// with *owned = true that the caller releases with hipFreeAsync on `st`.
-enum WsSlot : int { WS_SPLITK = 0, WS_GLU = 1, WS_OFFSETS = 2, WS_SORT = 3 };
-hipError_t workspace_get(hipStream_t st, int slot, size_t bytes, void** p, bool* owned);
+// Scratch of one call: the (device, stream, slot) buffer, grown outside
+// capture; during capture a request larger than the buffer fails with
+// hipErrorStreamCaptureUnsupported (nothing is allocated inside a graph).
+enum WsSlot : int { WS_SPLITK = 0, WS_GLU = 1, WS_OFFSETS = 2, WS_SORT = 3, WS_NSLOTS = 4 };
+hipError_t workspace_get(hipStream_t st, int slot, size_t bytes, void** p);
+// grow every slot of the stream to at least `bytes` (outside capture)
+hipError_t workspace_reserve(hipStream_t st, size_t bytes);
 
 }  // namespace iqmm

@@ -371,8 +371,7 @@ hipError_t launch_moe_sort(const int32_t* experts, int n, int k, int E, int32_t*
   const int64_t L = (static_cast<int64_t>(E) + 1) * nb;
   if (n > 0 && L + 2 * SORT_BLOCK <= 16384) {
     void* ws = nullptr;
-    bool owned = false;
-    hipError_t e = workspace_get(st, WS_SORT, static_cast<size_t>(L) * 4, &ws, &owned);
+    hipError_t e = workspace_get(st, WS_SORT, static_cast<size_t>(L) * 4, &ws);
     if (e != hipSuccess) return e;
     int32_t* hist = static_cast<int32_t*>(ws);
     hipLaunchKernelGGL(moe_count_kernel, dim3(nb), dim3(SORT_BLOCK), static_cast<size_t>(E + 1) * 4, st, experts, n,
@@ -384,8 +383,7 @@ hipError_t launch_moe_sort(const int32_t* experts, int n, int k, int E, int32_t*
                          inverse, offsets);
       e = hipGetLastError();
     }
-    const hipError_t f = owned ? hipFreeAsync(ws, st) : hipSuccess;
-    return e != hipSuccess ? e : f;
+    return e;
   }
   int np = 2;
   while (np < n) np <<= 1;

@@ -989,8 +989,7 @@ template <int XT, class F>
 hipError_t splitk_run(const QmmArgs& a, int ks, F&& launch) {
   const int64_t n = static_cast<int64_t>(a.nbatch) * a.M * a.N;
   void* ws = nullptr;
-  bool owned = false;
-  hipError_t e = workspace_get(a.stream, WS_SPLITK, static_cast<size_t>(n) * ks * sizeof(float), &ws, &owned);
+  hipError_t e = workspace_get(a.stream, WS_SPLITK, static_cast<size_t>(n) * ks * sizeof(float), &ws);
   if (e != hipSuccess) return e;
   float* part = static_cast<float*>(ws);
   e = launch(part);
@@ -1000,8 +999,7 @@ hipError_t splitk_run(const QmmArgs& a, int ks, F&& launch) {
                        static_cast<uint16_t*>(a.out), n, ks);
     e = hipGetLastError();
   }
-  const hipError_t f = owned ? hipFreeAsync(part, a.stream) : hipSuccess;
-  return e != hipSuccess ? e : f;
+  return e;
 }
 
 template <int XT, int MODE, int BITS, int TM, int TN>

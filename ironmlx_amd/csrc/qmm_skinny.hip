@@ -1087,8 +1087,7 @@ hipError_t launch_gather_sorted(const QmmArgs& a, int64_t nflat, int64_t E) {
   if (E + 1 > 65535) return hipErrorInvalidConfiguration;
   // segment offsets in the stream's offsets workspace (workspace.hip)
   void* ws = nullptr;
-  bool owned = false;
-  hipError_t e = workspace_get(a.stream, WS_OFFSETS, static_cast<size_t>(E + 1) * sizeof(int64_t), &ws, &owned);
+  hipError_t e = workspace_get(a.stream, WS_OFFSETS, static_cast<size_t>(E + 1) * sizeof(int64_t), &ws);
   if (e != hipSuccess) return e;
   int64_t* off = static_cast<int64_t*>(ws);
   const int64_t nb = (nflat + 1 + 255) / 256;
@@ -1096,8 +1095,7 @@ hipError_t launch_gather_sorted(const QmmArgs& a, int64_t nflat, int64_t E) {
                      a.bm.rhs_dt, nflat, E, off);
   e = hipGetLastError();
   if (e == hipSuccess) e = a.xdt == BF16 ? gather_by_mode<BF16>(a, nflat, E, off) : gather_by_mode<F16>(a, nflat, E, off);
-  const hipError_t f = owned ? hipFreeAsync(off, a.stream) : hipSuccess;
-  return e != hipSuccess ? e : f;
+  return e;
 }
 
 hipError_t launch_qmm_skinny(const QmmArgs& a) {

@@ -1,21 +1,24 @@
 // workspace.hip — device workspaces of the calls that need scratch memory
 // (split-K partial sums, the gate_up product of a generic fused SwiGLU, the
-// expert segment offsets of a grouped gather).
+// expert segment offsets of a grouped gather, the bucket counts of the MoE
+// sort).
 //
 // Each (device, stream, slot) keeps one grow-only buffer, taken from the
 // stream-ordered pool (hipMallocAsync on that stream, so it is ordered after
 // the stream's earlier work) and never freed: HIP graphs captured on the
-// stream keep pointing at it, so their replays need no allocation nodes
-// (measured ~8 us per captured split-K call otherwise).  Calls on one stream
-// execute in order, so they can share its buffers; a graph captured on a
-// stream uses that stream's buffers and must not be replayed concurrently
-// with other work on that stream.  During capture a buffer cannot grow; a
-// larger request then falls back to a per-call hipMallocAsync / hipFreeAsync
-// pair (an allocation node in the graph).
+// stream keep pointing at it, so they hold kernel nodes only.  Calls on one
+// stream execute in order, so they can share its buffers; a graph captured on
+// a stream uses that stream's buffers and must not be replayed concurrently
+// with other library work on that stream, or with another graph captured on
+// it.  Nothing is allocated during capture (policy in workspace_core.h): a
+// request that the buffer cannot hold then fails with
+// hipErrorStreamCaptureUnsupported, and the caller sizes the buffers first
+// (an eager call of the same shapes on the stream, or workspace_reserve).
 #include <mutex>
 #include <unordered_map>
 
 #include "launch.h"
+#include "workspace_core.h"
 
 namespace iqmm {
 namespace {
@@ -45,28 +48,25 @@ std::unordered_map<Key, Buf, KeyHash>& table() {
 
 }  // namespace
 
-hipError_t workspace_get(hipStream_t st, int slot, size_t bytes, void** p, bool* owned) {
+hipError_t workspace_get(hipStream_t st, int slot, size_t bytes, void** p) {
   *p = nullptr;
-  *owned = false;
-  if (bytes == 0) bytes = 256;
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
   e = hipStreamIsCapturing(st, &cs);
   if (e != hipSuccess) return e;
-  {
-    std::lock_guard<std::mutex> lk(g_mu);
-    Buf& b = table()[Key{dev, st, slot}];
-    if (b.cap >= bytes) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  Buf& b = table()[Key{dev, st, slot}];
+  switch (ws_decide(b.cap, bytes, cs != hipStreamCaptureStatusNone)) {
+    case WsDecision::Reuse:
       *p = b.p;
       return hipSuccess;
-    }
-    if (cs == hipStreamCaptureStatusNone) {
-      // grow (x2 steps, 1 MiB minimum); the old buffer stays allocated for
-      // graphs that captured it
-      size_t cap = b.cap ? b.cap : (size_t{1} << 20);
-      while (cap < bytes) cap *= 2;
+    case WsDecision::CaptureTooSmall:
+      return hipErrorStreamCaptureUnsupported;
+    case WsDecision::Grow: {
+      // the old buffer stays allocated: graphs captured earlier point at it
+      const size_t cap = ws_grown_cap(b.cap, bytes);
       void* np = nullptr;
       e = hipMallocAsync(&np, cap, st);
       if (e != hipSuccess) return e;
@@ -76,10 +76,16 @@ hipError_t workspace_get(hipStream_t st, int slot, size_t bytes, void** p, bool*
       return hipSuccess;
     }
   }
-  // capturing and the buffer is too small: a per-call stream-ordered allocation
-  e = hipMallocAsync(p, bytes, st);
-  if (e == hipSuccess) *owned = true;
-  return e;
+  return hipErrorUnknown;
+}
+
+hipError_t workspace_reserve(hipStream_t st, size_t bytes) {
+  for (int slot = 0; slot < WS_NSLOTS; ++slot) {
+    void* p = nullptr;
+    const hipError_t e = workspace_get(st, slot, bytes, &p);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 }  // namespace iqmm

@@ -251,3 +251,12 @@ def quantize(w: torch.Tensor, group_size: Optional[int] = None, bits: Optional[i
 __all__ = ["quantized_matmul", "dequantize", "gather_qmm", "quantize", "quantized_swiglu",
            "gather_qmm_swiglu", "dequantize_rows", "moe_route", "moe_sort", "moe_combine",
            "IqmmError"]
+
+
+def workspace_reserve(nbytes: int, stream=None, device=None) -> None:
+    """Grow every library workspace of ``stream`` (default: the current stream)
+    to at least ``nbytes`` so that calls later captured into a HIP graph on that
+    stream allocate nothing (the library never allocates while capturing)."""
+    L = _lib.load()
+    dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+    _lib.check(L.iqmm_workspace_reserve(_stream(dev, stream), int(nbytes)))

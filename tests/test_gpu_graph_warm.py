@@ -91,3 +91,61 @@ def test_graph_moe_block(ops, cap_stream):
 
     print("graph: MoE block E=256 H=2048 I=512 k=8 T=64", flush=True)
     _check_warm_graph(block, cap_stream)
+
+
+def test_capture_on_unsized_stream_raises(ops):
+    """Nothing is allocated during capture: on a stream whose split-K
+    workspace was never sized, the captured call fails with a message (the
+    request is refused before any kernel is enqueued)."""
+    from ironmlx_amd._lib import IqmmError
+    gen = torch.Generator(device="cuda").manual_seed(24)
+    w, s, b = _weight(gen, (), 4096, 4096)
+    x = torch.randn((256, 4096), generator=gen, device="cuda").to(torch.bfloat16)
+    fresh = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    print("graph: split-K GEMM captured on an unsized stream (must raise)", flush=True)
+    with pytest.raises(IqmmError, match="during graph capture"):
+        with torch.cuda.graph(g, stream=fresh):
+            ops.quantized_matmul(x, w, s, b, True, 64, 4)
+    torch.cuda.synchronize()
+
+
+def test_reserved_stream_capture_with_eager_work_between_replays(ops):
+    """iqmm_workspace_reserve sizes a fresh stream's workspaces, so the calls
+    captured on it hold kernel nodes only; eager allocation and
+    synchronisation between replays leave every replay bit-identical."""
+    from ironmlx_amd import nn
+    gen = torch.Generator(device="cuda").manual_seed(25)
+    w, s, b = _weight(gen, (), 4096, 4096)
+    x = torch.randn((256, 4096), generator=gen, device="cuda").to(torch.bfloat16)
+    gu = _weight(gen, (), 2 * 14336, 4096)
+    x4 = torch.randn((4, 4096), generator=gen, device="cuda").to(torch.bfloat16)
+    E, H, I, k, T = 256, 2048, 512, 8, 64
+    experts = {"gate_up": nn.StackedExperts(*_weight(gen, (E,), 2 * I, H)),
+               "down": nn.StackedExperts(*_weight(gen, (E,), H, I))}
+    moe = nn.MoEMLP(None, experts, None, None, k, True)
+    logits = torch.randn((T, E), generator=gen, device="cuda").to(torch.bfloat16)
+    xm = torch.randn((T, H), generator=gen, device="cuda").to(torch.bfloat16)
+
+    def fn():
+        sc, ex = ops.moe_route(logits, k, True)
+        return (ops.quantized_matmul(x, w, s, b, True, 64, 4),
+                ops.quantized_swiglu(x4, *gu, 64, 4),
+                moe.experts_forward(xm, sc, ex), sc, ex)
+
+    ref = [t.clone() for t in fn()]
+    stream = torch.cuda.Stream()
+    ops.workspace_reserve(64 << 20, stream=stream)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    print("graph: reserved stream, split-K GEMM + SwiGLU M=4 + MoE block T=64", flush=True)
+    with torch.cuda.graph(g, stream=stream):
+        outs = fn()
+    for r in range(3):
+        junk = torch.randn(1 << 20, device="cuda") * float(r + 1)
+        junk.sum().item()
+        g.replay()
+        torch.cuda.synchronize()
+        for i, (o, e) in enumerate(zip(outs, ref)):
+            assert torch.equal(_bits(o), _bits(e)), f"replay {r}, output {i}"

@@ -117,6 +117,40 @@ def test_gather_qmm_swiglu(ops, dt, T, sorted_):
     assert np.array_equal(_bits(got, dt).reshape(T * k, I), np.ascontiguousarray(ref).view(np.uint16))
 
 
+@pytest.mark.parametrize("gs,I", [(32, 512), (128, 512), (64, 520), (32, 520), (128, 520)])
+@pytest.mark.parametrize("T", [64, 512])
+def test_gather_qmm_swiglu_group_sizes(ops, gs, I, T):
+    """The grouped SwiGLU epilogue at every group size (gs 32: four groups per
+    128-code chunk group, gs 128: one) and with a ragged I (not a multiple of
+    the 32-column tile): bit-exact with the oracle's SwiGLU of the gather_qmm
+    product."""
+    print(f"gather swiglu gs={gs} I={I} T={T}", flush=True)
+    dt = "bf16"
+    rng = np.random.default_rng(gs + I + T)
+    E, H, k = 32, 2048, 8
+    wn, sn, bn = rand_affine(rng, 2 * I, H, gs, 4, dt, (E,))
+    w, s, b = words_to_torch(wn), from_np(sn, dt), from_np(bn, dt)
+    x = torch.randn(T, 1, H, generator=torch.Generator().manual_seed(T + gs)).to(TDT[dt]).cuda()
+    ex = torch.from_numpy(np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32))
+    flat = ex.reshape(-1)
+    order = torch.argsort(flat, stable=True)
+    rhs = flat[order].contiguous().cuda()
+    lhs = (order // k).to(torch.int32).contiguous().cuda()
+    got = ops.gather_qmm_swiglu(x, w, s, b, lhs, rhs, gs, 4, sorted_indices=True)
+    gu = ops.gather_qmm(x, w, s, b, lhs, rhs, True, gs, 4, sorted_indices=True)
+    torch.cuda.synchronize()
+    ref = oracle.swiglu(to_np(gu, dt).reshape(T * k, 2 * I), dt)
+    assert np.array_equal(_bits(got, dt).reshape(T * k, I), np.ascontiguousarray(ref).view(np.uint16))
+    # and the product itself against the oracle's per-row products
+    xs = to_np(x[:, 0], dt)[(order // k).numpy()]
+    rn = rhs.cpu().numpy()
+    refp = np.zeros((T * k, 2 * I))
+    for e in np.unique(rn):
+        rows = np.nonzero(rn == e)[0]
+        refp[rows] = oracle.qmv_affine(xs[rows], dt, wn[e], sn[e], bn[e], dt, gs, 4, odt="f32", nthreads=8)
+    assert rel_err(as_f64(to_np(gu, dt).reshape(T * k, 2 * I), dt), refp) <= 1e-2
+
+
 # ------------------------------------------------------------------ row gather
 @pytest.mark.parametrize("mode,bits,gs", [("affine", 4, 64), ("affine", 3, 32), ("affine", 8, 128),
                                           ("mxfp4", 4, 32), ("mxfp8", 8, 32), ("nvfp4", 4, 16)])
