@@ -228,6 +228,23 @@ int iqmm_moe_sort(iqmm_array* res_tokens, iqmm_array* res_sorted, iqmm_array* re
                   iqmm_array* res_offsets, iqmm_array experts, int num_experts, iqmm_stream stream);
 
 /*
+ * iqmm_moe_sort with no allocation: the same arguments, results and limits,
+ * bit-identical output.  No counterpart in the reference or mlx-c; it is for
+ * callers that cannot allocate device memory (code under HIP graph capture on
+ * a stream whose workspaces were never sized, tight serving loops, harnesses
+ * that forbid hipMalloc).  The counting sort's (bucket, block) counts,
+ * (num_experts + 1) * ceil(n / 256) int32, live in one fixed per-device array
+ * of 15872 int32 (62 KiB, held until the process ends); a routing that needs
+ * more takes the one-workgroup bitonic sort, which uses no scratch, and
+ * n > 32768 is rejected as by iqmm_moe_sort.  Calls on one GPU share that
+ * array: two calls that overlap in time on one GPU (different streams, or
+ * graphs replayed concurrently) race on it.
+ */
+int iqmm_moe_sort_noalloc(iqmm_array* res_tokens, iqmm_array* res_sorted, iqmm_array* res_inverse,
+                          iqmm_array* res_offsets, iqmm_array experts, int num_experts,
+                          iqmm_stream stream);
+
+/*
  * Weighted combine of expert outputs: out[t, :] = sum over the k slots of t,
  * in ascending expert order, of float32(y[inverse[t*k + slot], :]) * score,
  * accumulated sequentially in float32 as mlx/src/nn/moe.rs:146-168 does.

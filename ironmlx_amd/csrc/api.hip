@@ -278,6 +278,42 @@ int qmm_common(const char* op, iqmm_array* res, const iqmm_array& x, const iqmm_
   return 0;
 }
 
+int moe_sort_entry(const char* op, bool noalloc, iqmm_array* res_tokens, iqmm_array* res_sorted,
+                   iqmm_array* res_inverse, iqmm_array* res_offsets, iqmm_array experts, int num_experts,
+                   iqmm_stream stream) {
+  g_last_error.clear();
+  if (!present(experts) || experts.ndim != 2 || experts.dtype != IQMM_INT32)
+    return fail("[%s] experts must be a 2D int32 array [tokens, k], got %s %s.", op, shape_str(experts).c_str(),
+                dt_name(experts.dtype));
+  if (num_experts < 1 || num_experts > 65535) return fail("[%s] num_experts must be in [1, 65535], got %d.", op, num_experts);
+  const int64_t n = numel(experts), k = experts.shape[1];
+  if (n > 32768) return fail("[%s] at most 32768 (token, slot) rows are sorted in one call, got %lld.", op, (long long)n);
+  const std::vector<int64_t> shp = {n}, oshp = {static_cast<int64_t>(num_experts) + 1};
+  bool q1, q2, q3, q4 = false;
+  if (set_or_check_res(op, res_tokens, shp, IQMM_INT32, &q1)) return 1;
+  if (set_or_check_res(op, res_sorted, shp, IQMM_INT32, &q2)) return 1;
+  if (set_or_check_res(op, res_inverse, shp, IQMM_INT32, &q3)) return 1;
+  if (res_offsets && set_or_check_res(op, res_offsets, oshp, IQMM_INT32, &q4)) return 1;
+  if (q1 || q2 || q3 || q4) {
+    if (!(q1 && q2 && q3 && (!res_offsets || q4))) return fail("[%s] either all result buffers are allocated or none.", op);
+    return 0;
+  }
+  if (n == 0) {
+    if (!res_offsets) return 0;
+    // int32 zeros have the bits of float32 zeros; a fill kernel (not a
+    // memset node) keeps the call capturable in a HIP graph
+    hipError_t e = fill_zero(res_offsets->data, IQMM_FLOAT32, static_cast<int64_t>(num_experts) + 1,
+                             static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? 0 : hip_fail(op, e);
+  }
+  hipError_t e = (noalloc ? launch_moe_sort_noalloc : launch_moe_sort)(
+      static_cast<const int32_t*>(experts.data), static_cast<int>(n), static_cast<int>(k), num_experts,
+      static_cast<int32_t*>(res_tokens->data), static_cast<int32_t*>(res_sorted->data),
+      static_cast<int32_t*>(res_inverse->data), res_offsets ? static_cast<int32_t*>(res_offsets->data) : nullptr,
+      static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? 0 : hip_fail(op, e);
+}
+
 }  // namespace
 }  // namespace iqmm
 
@@ -641,38 +677,14 @@ int iqmm_moe_route(iqmm_array* res_scores, iqmm_array* res_experts, iqmm_array l
 
 int iqmm_moe_sort(iqmm_array* res_tokens, iqmm_array* res_sorted, iqmm_array* res_inverse,
                   iqmm_array* res_offsets, iqmm_array experts, int num_experts, iqmm_stream stream) {
-  const char* op = "moe_sort";
-  g_last_error.clear();
-  if (!present(experts) || experts.ndim != 2 || experts.dtype != IQMM_INT32)
-    return fail("[%s] experts must be a 2D int32 array [tokens, k], got %s %s.", op, shape_str(experts).c_str(),
-                dt_name(experts.dtype));
-  if (num_experts < 1 || num_experts > 65535) return fail("[%s] num_experts must be in [1, 65535], got %d.", op, num_experts);
-  const int64_t n = numel(experts), k = experts.shape[1];
-  if (n > 32768) return fail("[%s] at most 32768 (token, slot) rows are sorted in one call, got %lld.", op, (long long)n);
-  const std::vector<int64_t> shp = {n}, oshp = {static_cast<int64_t>(num_experts) + 1};
-  bool q1, q2, q3, q4 = false;
-  if (set_or_check_res(op, res_tokens, shp, IQMM_INT32, &q1)) return 1;
-  if (set_or_check_res(op, res_sorted, shp, IQMM_INT32, &q2)) return 1;
-  if (set_or_check_res(op, res_inverse, shp, IQMM_INT32, &q3)) return 1;
-  if (res_offsets && set_or_check_res(op, res_offsets, oshp, IQMM_INT32, &q4)) return 1;
-  if (q1 || q2 || q3 || q4) {
-    if (!(q1 && q2 && q3 && (!res_offsets || q4))) return fail("[%s] either all result buffers are allocated or none.", op);
-    return 0;
-  }
-  if (n == 0) {
-    if (!res_offsets) return 0;
-    // int32 zeros have the bits of float32 zeros; a fill kernel (not a
-    // memset node) keeps the call capturable in a HIP graph
-    hipError_t e = fill_zero(res_offsets->data, IQMM_FLOAT32, static_cast<int64_t>(num_experts) + 1,
-                             static_cast<hipStream_t>(stream));
-    return e == hipSuccess ? 0 : hip_fail(op, e);
-  }
-  hipError_t e = launch_moe_sort(static_cast<const int32_t*>(experts.data), static_cast<int>(n), static_cast<int>(k),
-                                 num_experts, static_cast<int32_t*>(res_tokens->data),
-                                 static_cast<int32_t*>(res_sorted->data), static_cast<int32_t*>(res_inverse->data),
-                                 res_offsets ? static_cast<int32_t*>(res_offsets->data) : nullptr,
-                                 static_cast<hipStream_t>(stream));
-  return e == hipSuccess ? 0 : hip_fail(op, e);
+  return moe_sort_entry("moe_sort", false, res_tokens, res_sorted, res_inverse, res_offsets, experts,
+                        num_experts, stream);
+}
+
+int iqmm_moe_sort_noalloc(iqmm_array* res_tokens, iqmm_array* res_sorted, iqmm_array* res_inverse,
+                          iqmm_array* res_offsets, iqmm_array experts, int num_experts, iqmm_stream stream) {
+  return moe_sort_entry("moe_sort_noalloc", true, res_tokens, res_sorted, res_inverse, res_offsets, experts,
+                        num_experts, stream);
 }
 
 int iqmm_moe_combine(iqmm_array* res, iqmm_array y, iqmm_array inverse, iqmm_array experts,

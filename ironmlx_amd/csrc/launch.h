@@ -77,6 +77,9 @@ hipError_t launch_moe_route(const void* logits, int dt, float* scores, int32_t* 
                             bool norm, hipStream_t st);
 hipError_t launch_moe_sort(const int32_t* experts, int n, int k, int E, int32_t* tokens, int32_t* sorted,
                            int32_t* inverse, int32_t* offsets, hipStream_t st);
+// the same sort with its bucket counts in a fixed per-device array (allocates nothing)
+hipError_t launch_moe_sort_noalloc(const int32_t* experts, int n, int k, int E, int32_t* tokens, int32_t* sorted,
+                                   int32_t* inverse, int32_t* offsets, hipStream_t st);
 hipError_t launch_moe_combine(const void* y, int dt, const int32_t* inverse, const int32_t* experts,
                               const float* scores, float* out, int T, int k, int64_t D, int E, int64_t n,
                               hipStream_t st);

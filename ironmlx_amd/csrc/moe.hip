@@ -13,6 +13,7 @@
 //         product taken as is and each further one added, as the reference's
 //         row_sum chain does.
 #include <atomic>
+#include <mutex>
 
 #include "launch.h"
 
@@ -363,17 +364,52 @@ hipError_t launch_moe_route(const void* logits, int dt, float* scores, int32_t* 
   return hipErrorInvalidValue;
 }
 
-hipError_t launch_moe_sort(const int32_t* experts, int n, int k, int E, int32_t* tokens, int32_t* sorted,
-                           int32_t* inverse, int32_t* offsets, hipStream_t st) {
+namespace {
+
+// Fixed scratch of iqmm_moe_sort_noalloc: the (bucket, block) counts of the
+// counting sort, SORT_HIST_MAX int32 (62 KiB) per device, held until the
+// process ends.  Host code never passes `scratch` itself to a kernel: it is a
+// host-side stand-in; the device address comes from hipGetSymbolAddress,
+// once per device (sort_scratch).  Every call on a device shares the array.
+constexpr int SORT_HIST_MAX = 16384 - 2 * SORT_BLOCK;
+static __device__ __align__(256) int32_t scratch[SORT_HIST_MAX];
+
+constexpr int kMaxDevices = 64;
+
+hipError_t sort_scratch(int32_t** out) {
+  static std::mutex mu;
+  static int32_t* ptr[kMaxDevices] = {};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lk(mu);
+  if (ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    ptr[dev] = static_cast<int32_t*>(p);
+  }
+  *out = ptr[dev];
+  return hipSuccess;
+}
+
+// hist: the counting sort's (bucket, block) counts, or nullptr to take them
+// from the stream's workspace
+hipError_t moe_sort_impl(const int32_t* experts, int n, int k, int E, int32_t* tokens, int32_t* sorted,
+                         int32_t* inverse, int32_t* offsets, hipStream_t st, int32_t* hist) {
   // counting sort when the (bucket, block) histogram fits one workgroup's LDS
   // with its partials: 64 KiB
   const int nb = (n + SORT_BLOCK - 1) / SORT_BLOCK;
   const int64_t L = (static_cast<int64_t>(E) + 1) * nb;
-  if (n > 0 && L + 2 * SORT_BLOCK <= 16384) {
-    void* ws = nullptr;
-    hipError_t e = workspace_get(st, WS_SORT, static_cast<size_t>(L) * 4, &ws);
-    if (e != hipSuccess) return e;
-    int32_t* hist = static_cast<int32_t*>(ws);
+  if (n > 0 && L <= SORT_HIST_MAX) {
+    hipError_t e = hipSuccess;
+    if (hist == nullptr) {
+      void* ws = nullptr;
+      e = workspace_get(st, WS_SORT, static_cast<size_t>(L) * 4, &ws);
+      if (e != hipSuccess) return e;
+      hist = static_cast<int32_t*>(ws);
+    }
     hipLaunchKernelGGL(moe_count_kernel, dim3(nb), dim3(SORT_BLOCK), static_cast<size_t>(E + 1) * 4, st, experts, n,
                        E, nb, hist);
     e = hipGetLastError();
@@ -403,6 +439,22 @@ hipError_t launch_moe_sort(const int32_t* experts, int n, int k, int E, int32_t*
   hipLaunchKernelGGL(moe_sort_kernel, dim3(1), dim3(1024), lds, st, experts, n, k, E, np, tokens, sorted, inverse,
                      offsets);
   return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_moe_sort(const int32_t* experts, int n, int k, int E, int32_t* tokens, int32_t* sorted,
+                           int32_t* inverse, int32_t* offsets, hipStream_t st) {
+  return moe_sort_impl(experts, n, k, E, tokens, sorted, inverse, offsets, st, nullptr);
+}
+
+hipError_t launch_moe_sort_noalloc(const int32_t* experts, int n, int k, int E, int32_t* tokens, int32_t* sorted,
+                                   int32_t* inverse, int32_t* offsets, hipStream_t st) {
+  // the counts are fully overwritten by moe_count_kernel: nothing to clear
+  int32_t* hist = nullptr;
+  const hipError_t e = sort_scratch(&hist);
+  if (e != hipSuccess) return e;
+  return moe_sort_impl(experts, n, k, E, tokens, sorted, inverse, offsets, st, hist);
 }
 
 hipError_t launch_moe_combine(const void* y, int dt, const int32_t* inverse, const int32_t* experts,
