@@ -15,7 +15,9 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libiqmm.so")
-SOURCES = ["api.hip", "qmv.hip", "qmv_q4.hip", "qmm_mfma.hip", "qmm_gemm.hip", "qmm_skinny.hip", "convert.hip", "moe.hip", "workspace.hip"]
+SOURCES = ["api.hip", "qmv.hip", "qmv_q4.hip", "qmm_mfma.hip", "qmm_gemm.hip", "qmm_skinny.hip", "convert.hip", "moe.hip", "workspace.hip", "qmm_decode.hip"]
+# per-file flags: MFMA results in VGPRs (no AGPR round trip before the VALU epilogue)
+FILE_FLAGS = {"qmm_decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
@@ -26,7 +28,7 @@ FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
 
 def _compile(src: str) -> str:
     obj = os.path.join(OBJ, os.path.splitext(src)[0] + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [HIPCC, *FLAGS, *FILE_FLAGS.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
     p = subprocess.run(cmd, capture_output=True, text=True)
     if p.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{p.stderr}")

@@ -201,6 +201,7 @@ hipError_t fill_zero(void* p, int dt, int64_t n, hipStream_t st) {
 hipError_t run_qmm(QmmArgs& a) {
   if (qmv_q4_m1_supported(a)) return launch_qmv_q4_m1(a);
   if (qmv_q8_m1_supported(a)) return launch_qmv_q8_m1(a);
+  if (a.M >= 4 && qmm_decode_supported(a)) return launch_qmm_decode(a);
   if (a.nbatch <= 65535 && qmm_skinny_fac_supported(a)) return launch_qmm_skinny_fac(a);
   if (a.M >= 2 && a.M <= 64 && a.nbatch * ((a.M + 31) / 32) <= 65535 && qmm_skinny_supported(a))
     return launch_qmm_skinny(a);
@@ -224,6 +225,7 @@ template <class F>
 hipError_t run_glu(QmmArgs& a, bool try_fused, F&& product) {
   a.glu = 1;
   if (try_fused && qmv_q4_m1_supported(a)) return launch_qmv_q4_m1(a);
+  if (try_fused && a.M >= 2 && qmm_decode_supported(a)) return launch_qmm_decode(a);
   if (try_fused && a.nbatch <= 65535 && qmm_skinny_fac_supported(a)) return launch_qmm_skinny_fac(a);
   a.glu = 0;
   const int64_t I = a.N, rows = a.nbatch * a.M;

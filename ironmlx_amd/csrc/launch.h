@@ -61,6 +61,9 @@ bool qmm_skinny_supported(const QmmArgs& a);
 // factored affine 4-bit MFMA kernel for decode widths (x rows <= 4 m tiles, <= 32)
 hipError_t launch_qmm_skinny_fac(const QmmArgs& a);
 bool qmm_skinny_fac_supported(const QmmArgs& a);
+// affine 4-bit decode widths (M <= 32) on MFMA, scales read once per wave range
+hipError_t launch_qmm_decode(const QmmArgs& a);
+bool qmm_decode_supported(const QmmArgs& a);
 // sorted-expert grouped gather_qmm: nflat batch elements, E experts
 hipError_t launch_gather_sorted(const QmmArgs& a, int64_t nflat, int64_t E);
 bool gather_sorted_supported(const QmmArgs& a);
