@@ -272,8 +272,6 @@ int qmm_common(const char* op, iqmm_array* res, const iqmm_array& x, const iqmm_
     if (check_scales(op, q, w, s, b, N / q.gs, sdt)) return 1;
     if (N % 32 != 0) return fail("[%s] transpose=false requires the output width (%lld) to be a multiple of 32.", op, (long long)N);
   }
-  if (q.mode == AFFINE && *sdt != x.dtype)
-    return fail("[%s] x (%s) and scales (%s) must have the same dtype.", op, dt_name(x.dtype), dt_name(*sdt));
   if (K % 32 != 0) return fail("[%s] The reduction dimension K=%lld must be a multiple of 32.", op, (long long)K);
   if (M > 0x7fffffffLL || N > 0x7fffffffLL || K > 0x7fffffffLL) return fail("[%s] dimension too large.", op);
   (void)res;
@@ -341,6 +339,41 @@ int iqmm_workspace_reserve(iqmm_stream stream, size_t bytes) {
 
 namespace iqmm {
 namespace {
+// MLX promotes x, scales and biases to one type before the product
+// (result_type of x and scales, then the biases'): equal types stay, float32
+// wins, and float16 with bfloat16 gives float32.  Every mixed affine call
+// therefore computes in float32: x and / or the scales and biases are copied
+// to float32 (exact) into the stream's conversion workspace.
+int result_dtype(const QParams& q, int xdt, int sdt) {
+  return (q.mode == AFFINE && sdt != xdt) ? IQMM_FLOAT32 : xdt;
+}
+
+hipError_t promote_inputs(QmmArgs& a, const iqmm_array& x, const iqmm_array& s, const iqmm_array& b, int sdt) {
+  if (a.mode != AFFINE || sdt == x.dtype) return hipSuccess;
+  const int64_t nx = x.dtype == IQMM_FLOAT32 ? 0 : numel(x), ns = sdt == IQMM_FLOAT32 ? 0 : numel(s);
+  auto up = [](int64_t n) { return (n * 4 + 255) / 256 * 256; };
+  void* ws = nullptr;
+  hipError_t e = workspace_get(a.stream, WS_CONV, static_cast<size_t>(up(nx) + 2 * up(ns)), &ws);
+  if (e != hipSuccess) return e;
+  char* p = static_cast<char*>(ws);
+  if (nx) {
+    e = launch_cast_f32(x.data, x.dtype, reinterpret_cast<float*>(p), nx, a.stream);
+    if (e != hipSuccess) return e;
+    a.x = p;
+    p += up(nx);
+  }
+  if (ns) {
+    e = launch_cast_f32(s.data, sdt, reinterpret_cast<float*>(p), ns, a.stream);
+    if (e != hipSuccess) return e;
+    a.s = p;
+    e = launch_cast_f32(b.data, sdt, reinterpret_cast<float*>(p + up(ns)), ns, a.stream);
+    if (e != hipSuccess) return e;
+    a.b = p + up(ns);
+  }
+  a.xdt = IQMM_FLOAT32;
+  return hipSuccess;
+}
+
 // quantized_matmul, and with glu its fused SwiGLU form (N = 2I weight rows -> I outputs)
 int qmm_entry(const char* op, iqmm_array* res, iqmm_array x, iqmm_array w, iqmm_array scales,
               iqmm_array biases, bool transpose, iqmm_optional_int group_size,
@@ -381,14 +414,15 @@ int qmm_entry(const char* op, iqmm_array* res, iqmm_array x, iqmm_array w, iqmm_
     a.nbatch = 1;
     for (auto d : bshape) a.nbatch *= d;
   }
+  const int odt = result_dtype(q, x.dtype, sdt);
   bool query;
-  if (set_or_check_res(op, res, out_shape, x.dtype, &query)) return 1;
+  if (set_or_check_res(op, res, out_shape, odt, &query)) return 1;
   if (query) return 0;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t out_n = numel(*res);
   if (out_n == 0) return 0;
   if (K == 0) {
-    hipError_t e = fill_zero(res->data, x.dtype, out_n, st);
+    hipError_t e = fill_zero(res->data, odt, out_n, st);
     return e == hipSuccess ? 0 : hip_fail(op, e);
   }
   a.x = x.data; a.w = static_cast<const uint32_t*>(w.data); a.s = scales.data; a.b = biases.data;
@@ -404,7 +438,9 @@ int qmm_entry(const char* op, iqmm_array* res, iqmm_array x, iqmm_array w, iqmm_
   a.bm.nx = nxm; a.bm.nw = nwm; a.bm.lhs = nullptr; a.bm.rhs = nullptr;
   a.stream = st;
   (void)Nw;
-  hipError_t e = glu ? run_glu(a, true, [](QmmArgs& p) { return run_qmm(p); }) : run_qmm(a);
+  hipError_t e = promote_inputs(a, x, scales, biases, sdt);
+  if (e != hipSuccess) return hip_fail(op, e);
+  e = glu ? run_glu(a, true, [](QmmArgs& p) { return run_qmm(p); }) : run_qmm(a);
   return e == hipSuccess ? 0 : hip_fail(op, e);
 }
 }  // namespace
@@ -461,14 +497,15 @@ int gather_entry(const char* op, iqmm_array* res, iqmm_array x, iqmm_array w, iq
   std::vector<int64_t> out_shape = bshape;
   out_shape.push_back(M);
   out_shape.push_back(N);
+  const int odt = result_dtype(q, x.dtype, sdt);
   bool query;
-  if (set_or_check_res(op, res, out_shape, x.dtype, &query)) return 1;
+  if (set_or_check_res(op, res, out_shape, odt, &query)) return 1;
   if (query) return 0;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t out_n = numel(*res);
   if (out_n == 0) return 0;
   if (K == 0) {
-    hipError_t e = fill_zero(res->data, x.dtype, out_n, st);
+    hipError_t e = fill_zero(res->data, odt, out_n, st);
     return e == hipSuccess ? 0 : hip_fail(op, e);
   }
   a.x = x.data; a.w = static_cast<const uint32_t*>(w.data); a.s = scales.data; a.b = biases.data;
@@ -488,6 +525,10 @@ int gather_entry(const char* op, iqmm_array* res, iqmm_array x, iqmm_array w, iq
   a.bm.rhs = present(rhs) ? rhs.data : nullptr;
   a.bm.lhs_dt = lhs.dtype; a.bm.rhs_dt = rhs.dtype;
   a.stream = st;
+  {
+    const hipError_t pe = promote_inputs(a, x, scales, biases, sdt);
+    if (pe != hipSuccess) return hip_fail(op, pe);
+  }
   // sorted form: rhs (and lhs, or x's batch when lhs is absent) enumerate the
   // output batch one-to-one, so expert segments are contiguous in it
   const bool one_to_one = present(rhs) && numel(rhs) == a.nbatch &&

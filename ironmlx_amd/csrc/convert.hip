@@ -287,6 +287,22 @@ __global__ __launch_bounds__(256) void swiglu_rows_kernel(const typename Store<D
   out[i] = swiglu_out<DT>(to_f<DT>(src[c]), to_f<DT>(src[n + c]));
 }
 
+// x / scales / biases of a mixed-dtype call, upcast to float32 (exact)
+__global__ __launch_bounds__(256) void cast_f32_kernel(const uint16_t* src, int sdt, float* dst, int64_t n) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += stride)
+    dst[i] = sdt == F16 ? h_to_f(src[i]) : bf16_to_f(src[i]);
+}
+
+hipError_t launch_cast_f32(const void* src, int sdt, float* dst, int64_t n, hipStream_t st) {
+  if (n == 0) return hipSuccess;
+  if (sdt != F16 && sdt != BF16) return hipErrorInvalidValue;
+  const int64_t nb = (n + 255) / 256;
+  const unsigned grid = static_cast<unsigned>(nb < 65536 ? nb : 65536);
+  hipLaunchKernelGGL(cast_f32_kernel, dim3(grid), dim3(256), 0, st, static_cast<const uint16_t*>(src), sdt, dst, n);
+  return hipGetLastError();
+}
+
 hipError_t launch_swiglu_rows(const void* gu, void* out, int64_t rows, int64_t n, int dt,
                               hipStream_t st) {
   const int64_t tot = rows * n;

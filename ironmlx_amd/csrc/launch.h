@@ -72,6 +72,8 @@ bool gather_sorted_glu_supported(const QmmArgs& a);
 bool qmm_gemm_supported(const QmmArgs& a);
 hipError_t launch_dequantize(const ConvArgs& a);
 hipError_t launch_quantize(const ConvArgs& a);
+// float16 / bfloat16 -> float32 copy (mixed-dtype calls)
+hipError_t launch_cast_f32(const void* src, int sdt, float* dst, int64_t n, hipStream_t st);
 // SwiGLU over a [rows, 2N] product (gate | up halves) -> [rows, N]
 hipError_t launch_swiglu_rows(const void* gu, void* out, int64_t rows, int64_t n, int dt,
                               hipStream_t st);
@@ -89,7 +91,7 @@ hipError_t launch_moe_combine(const void* y, int dt, const int32_t* inverse, con
 // Scratch of one call: the (device, stream, slot) buffer, grown outside
 // capture; during capture a request larger than the buffer fails with
 // hipErrorStreamCaptureUnsupported (nothing is allocated inside a graph).
-enum WsSlot : int { WS_SPLITK = 0, WS_GLU = 1, WS_OFFSETS = 2, WS_SORT = 3, WS_NSLOTS = 4 };
+enum WsSlot : int { WS_SPLITK = 0, WS_GLU = 1, WS_OFFSETS = 2, WS_SORT = 3, WS_CONV = 4, WS_NSLOTS = 5 };
 hipError_t workspace_get(hipStream_t st, int slot, size_t bytes, void** p);
 // grow every slot of the stream to at least `bytes` (outside capture)
 hipError_t workspace_reserve(hipStream_t st, size_t bytes);

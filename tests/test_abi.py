@@ -107,8 +107,6 @@ def test_rejects_shapes_and_dtypes():
     assert rc != 0 and "expected number of groups" in err
     rc, _, err = qmm_query(A((1, 4096), F16), w, s, NONE)
     assert rc != 0 and "Biases must be provided" in err
-    rc, _, err = qmm_query(A((1, 4096), BF16), w, s, b)
-    assert rc != 0 and "same dtype" in err
     rc, _, err = qmm_query(A((1, 4096), F16), A((64, 512), F32), s, b)
     assert rc != 0 and "uint32" in err
     rc, _, err = qmm_query(A((1, 4096), BF16), A((64, 1024), U32), A((64, 128), U8),
@@ -117,6 +115,21 @@ def test_rejects_shapes_and_dtypes():
     rc, _, err = qmm_query(A((2, 1, 64), F16), A((3, 8, 8), U32), A((3, 8, 1), F16),
                            A((3, 8, 1), F16), gs=64)
     assert rc != 0 and "broadcast" in err
+
+
+@pytest.mark.parametrize("xdt,sdt,odt", [(BF16, F16, F32), (F16, BF16, F32), (F32, BF16, F32),
+                                         (F32, F16, F32), (BF16, F32, F32), (BF16, BF16, BF16),
+                                         (F16, F16, F16), (F32, F32, F32)])
+def test_mixed_dtype_promotion(xdt, sdt, odt):
+    """x and affine scales of different types promote as MLX promotes them
+    (equal types stay; float32 wins; float16 with bfloat16 gives float32)."""
+    w, s, b = A((64, 512), U32), A((64, 64), sdt), A((64, 64), sdt)
+    rc, res, err = qmm_query(A((3, 4096), xdt), w, s, b)
+    assert rc == 0, err
+    assert res.dtype == odt and shape_of(res) == (3, 64)
+    # fp modes keep x's type (uint8 scales)
+    rc, res, err = qmm_query(A((1, 4096), F32), A((64, 1024), U32), A((64, 128), U8), NONE, mode=b"mxfp8")
+    assert rc == 0 and res.dtype == F32
 
 
 def test_result_buffer_mismatch_is_rejected():

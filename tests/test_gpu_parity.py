@@ -489,3 +489,50 @@ def test_decode_width_and_gather_misaligned_scales(ops, gs):
     g1 = ops.gather_qmm(xg, tw2, _misaligned(ts2), _misaligned(tb2), None, rhs, True, gs, 4, "affine", True)
     g0 = ops.gather_qmm(xg, tw2, ts2, tb2, None, rhs, True, gs, 4, "affine", True)
     assert rel_err(as_f64(to_np(g1, "bf16"), "bf16"), as_f64(to_np(g0, "bf16"), "bf16")) <= TOL["bf16"]
+
+
+# ------------------------------------------------------------------ mixed dtypes
+@pytest.mark.parametrize("xdt,sdt", [("f32", "bf16"), ("f32", "f16"), ("f16", "bf16"), ("bf16", "f16"),
+                                     ("bf16", "f32")])
+@pytest.mark.parametrize("M", [1, 5, 70])
+def test_mixed_dtype_promotes_to_f32(ops, xdt, sdt, M):
+    """MLX casts x, scales and biases to their promoted type (float32 for any
+    mixed pair) before the product (mlx/src/nn/linear.rs:51-63 passes x in
+    whatever type the model produces).  The result is float32 and equals the
+    oracle's float32 product of the exactly upcast operands."""
+    print(f"mixed x={xdt} scales={sdt} M={M}", flush=True)
+    rng = np.random.default_rng(M + len(xdt) * 7 + len(sdt))
+    N, K = 96, 512
+    w, s, b = rand_affine(rng, N, K, 64, 4, sdt)
+    x = oracle.from_float(rng.standard_normal((M, K)).astype(np.float32), xdt)
+    got = ops.quantized_matmul(from_np(x, xdt), words_to_torch(w), from_np(s, sdt), from_np(b, sdt),
+                               True, 64, 4)
+    assert got.dtype == torch.float32
+    up = lambda a, dt: oracle.to_float(a, dt).astype(np.float32)  # noqa: E731
+    ref = oracle.qmm(up(x, xdt), "f32", w, up(s, sdt), up(b, sdt), "f32", True, 64, 4, odt="f32")
+    assert rel_err(got.cpu().numpy(), ref) <= 1e-5
+
+
+def test_mixed_dtype_gather_and_swiglu(ops):
+    """gather_qmm and the fused SwiGLU follow the same promotion."""
+    rng = np.random.default_rng(5)
+    E, N, K, T = 4, 64, 256, 6
+    w, s, b = rand_affine(rng, N * E, K, 64, 4, "bf16")
+    wt, st, bt = (words_to_torch(w).view(E, N, -1), from_np(s, "bf16").view(E, N, -1),
+                  from_np(b, "bf16").view(E, N, -1))
+    x = rng.standard_normal((T, 1, K)).astype(np.float32)
+    idx = torch.tensor([3, 0, 1, 1, 2, 0], dtype=torch.int32, device="cuda")
+    got = ops.gather_qmm(torch.from_numpy(x).cuda(), wt, st, bt, None, idx)
+    assert got.dtype == torch.float32
+    up = lambda a: oracle.to_float(a, "bf16").astype(np.float32)  # noqa: E731
+    wn, sn, bn = w.reshape(E, N, -1), s.reshape(E, N, -1), b.reshape(E, N, -1)
+    for i, e in enumerate(idx.tolist()):
+        ref = oracle.qmm(x[i], "f32", wn[e], up(sn[e]), up(bn[e]), "f32", True, 64, 4, odt="f32")
+        assert rel_err(got[i].cpu().numpy(), ref) <= 1e-5
+    # SwiGLU over [2I, K]: f32 x with bf16 scales gives float32 silu(gate) * up
+    gu = ops.quantized_swiglu(torch.from_numpy(x[:, 0]).cuda(), words_to_torch(w[:2 * N]),
+                              from_np(s[:2 * N], "bf16"), from_np(b[:2 * N], "bf16"), 64, 4)
+    assert gu.dtype == torch.float32
+    prod = oracle.qmm(x[:, 0], "f32", w[:2 * N], up(s[:2 * N]), up(b[:2 * N]), "f32", True, 64, 4, odt="f32")
+    ref = oracle.swiglu(prod, "f32").astype(np.float64)
+    assert rel_err(gu.cpu().numpy(), ref) <= 1e-5
