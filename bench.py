@@ -561,6 +561,16 @@ def run_only(ops, args):
         return {"only": "llama", **bench_llama_decode(ops)}
     if args.only == "widths":
         return {"only": "widths", **bench_decode_widths(ops)}
+    if args.only == "decode":
+        # the decode-width kernel at the Llama-3-8B gate/up and down shapes
+        res = {}
+        for (N, K, M) in ((14336, 4096, 16), (14336, 4096, 32), (4096, 14336, 16)):
+            r = bench_gemv(ops, args.steps, args.warmup, M=M, N=N, K=K)
+            res[f"M{M}_N{N}_K{K}"] = {"us": round(r["avg_launch_us"], 2), "gbs": round(r["kernel_gbs"], 1),
+                                      "bytes_per_launch": r["bytes_per_launch"]}
+        return {"only": "decode", **res}
+    if args.only == "moe512":
+        return {"only": "moe512", **bench_moe(ops, Ts=(512,))}
     nbytes = 256 << 20
     a = torch.empty(nbytes // 4, dtype=torch.int32, device="cuda").fill_(1)
     b = torch.empty_like(a)
@@ -590,7 +600,7 @@ def main():
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-widths", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--only", choices=["gemv", "prefill", "moe", "sweep", "fused", "llama", "widths", "copy"], default=None,
+    ap.add_argument("--only", choices=["gemv", "prefill", "moe", "sweep", "fused", "llama", "widths", "decode", "moe512", "copy"], default=None,
                     help="run one workload (for rocprofv3 kernel-trace / counter passes)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -614,6 +624,9 @@ def main():
     widths = None if args.no_widths else bench_decode_widths(ops)
     llama = None if args.no_llama else bench_llama_decode(ops)
     fused = bench_fused(ops)
+    # tied lm_head of Llama-3-8B (LinearLayer::from_weights on model.embed_tokens,
+    # mlx/src/model/llama.rs:158-162): the largest GEMV of a decode step
+    lmh = bench_gemv(ops, max(3, args.steps // 4), args.warmup, M=1, N=128256, K=4096)
     tr = load_traffic()
     traffic = tr.get("gemv_q4_gs64_k4096_n14336_m1", {}).get("traffic_bytes")
     traffic_pf = tr.get("prefill_q4_gs64_m2048_k4096_n14336", {}).get("traffic_bytes")
@@ -653,6 +666,10 @@ def main():
                     "down_proj_K14336_N4096_tflops": round(prefill_down["kernel_tflops"], 2),
                     "down_proj_avg_launch_us": round(prefill_down["kernel_us"], 2)},
         "moe_gather_qmm": moe,
+        "lm_head_gemv_n128256_k4096_m1": {"us": round(lmh["avg_launch_us"], 2),
+                                          "gbs": round(lmh["kernel_gbs"], 1),
+                                          "hbm_frac": round(lmh["kernel_gbs"] / HBM_PEAK_GBS, 4),
+                                          "bytes_per_launch": lmh["bytes_per_launch"]},
         "fused_paths": fused,
     }
     if sweep is not None:
