@@ -64,6 +64,9 @@ bool qmm_skinny_fac_supported(const QmmArgs& a);
 // affine 4-bit decode widths (M <= 32) on MFMA, scales read once per wave range
 hipError_t launch_qmm_decode(const QmmArgs& a);
 bool qmm_decode_supported(const QmmArgs& a);
+// grouped gather_qmm with the decode kernel's factored arithmetic (affine 4-bit)
+hipError_t launch_gather_decode(const QmmArgs& a, int64_t nflat, int64_t E, const int64_t* off);
+bool gather_decode_supported(const QmmArgs& a);
 // sorted-expert grouped gather_qmm: nflat batch elements, E experts
 hipError_t launch_gather_sorted(const QmmArgs& a, int64_t nflat, int64_t E);
 bool gather_sorted_supported(const QmmArgs& a);

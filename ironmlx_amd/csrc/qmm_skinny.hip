@@ -1094,7 +1094,10 @@ hipError_t launch_gather_sorted(const QmmArgs& a, int64_t nflat, int64_t E) {
   hipLaunchKernelGGL(segment_offsets_kernel, dim3(static_cast<unsigned>(nb)), dim3(256), 0, a.stream, a.bm.rhs,
                      a.bm.rhs_dt, nflat, E, off);
   e = hipGetLastError();
-  if (e == hipSuccess) e = a.xdt == BF16 ? gather_by_mode<BF16>(a, nflat, E, off) : gather_by_mode<F16>(a, nflat, E, off);
+  if (e == hipSuccess) {
+    if (gather_decode_supported(a)) e = launch_gather_decode(a, nflat, E, off);
+    else e = a.xdt == BF16 ? gather_by_mode<BF16>(a, nflat, E, off) : gather_by_mode<F16>(a, nflat, E, off);
+  }
   return e;
 }
 
