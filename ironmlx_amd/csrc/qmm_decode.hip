@@ -9,25 +9,31 @@
 //   sum x (s q + b) = s D + (b - C s) X,   D = sum x (C + q),  X = sum x,
 // with X from the same MFMA against an all-ones operand.  K slots are
 // chunk-major: MFMA j of a 128-code block takes chunk 4p + j (inside one
-// group for gs >= 32) and lane (r, q) its 8-code piece q, so an x load is 64
-// contiguous bytes per row; each lane loads one 16-byte weight chunk and a
-// 4 x 4 dword transpose across the lanes q (v_permlane32_swap, then
-// v_permlane16_swap) hands it out.
+// group for gs >= 32) and lane (r, q) its 8-code piece q; each lane reads one
+// 16-byte weight chunk and a 4 x 4 dword transpose across the lanes q
+// (v_permlane32_swap, then v_permlane16_swap) hands it out.
 //
 // A workgroup owns NT 16-row tiles (NC = 16 NT output columns) and its S waves
-// split K into S ranges of KB blocks each (KB is a template argument: the
-// K loop is fully unrolled and every offset is an immediate).  Each wave reads
-// the scale / bias words of its whole K range for its NT rows once (every lane
-// of a row loads the same words), keeps D blocks of x and weights in flight,
-// and leaves NT x MT 16 x 16 fp32 partial tiles that meet in LDS.  Rows past M
-// read the last x row and produce output rows that are never stored, so no
-// per-element masking is needed.  GLU: the weight holds 2N rows (gate rows
-// [0, N), up rows [N, 2N)); tiles [0, NT/2) take gate rows and [NT/2, NT) the
+// split K into ranges of KB blocks (a template argument: the K loop is fully
+// unrolled).  Each wave streams its range in stages of two blocks through a
+// ring of D stages in its own slice of LDS, filled by LDS DMA
+// (global_load_lds_dwordx4): weights as 8 rows x 128 B per instruction (whole
+// cache lines; 16 rows x 64 B straight into the MFMA layout measured 30%
+// slower on the read alone) and, with XL, x as 2 rows x 512 B, each row's
+// 16-byte pieces XOR-swizzled by the row so the MFMA-layout ds_read_b128 are
+// conflict-free.  Without XL, x fragments are loaded straight into registers
+// (16 rows x 64 B; cheaper where four tiles share each fragment).  Every
+// global load of the K loop is inline assembly with explicit vmcnt waits
+// (straight-line code, so each wait is exact).  Scale / bias words of the
+// wave's K range are read once per tile.  Rows past M read the last x row and
+// produce output rows that are never stored.  GLU: the weight holds 2N rows
+// (gate [0, N), up [N, 2N)); tiles [0, NT/2) take gate rows and [NT/2, NT) the
 // matching up rows, and the epilogue writes silu(gate) * up (NC = 8 NT).
 //
-// Measured against the previous decode-width kernel on MI355X (bf16, gs 64):
-// K = 4096, N = 14336: M = 4 / 16 / 32 17.9 / 20.2 / 23.5 -> 12.1 / 13.8 /
-// 17.5 us; N = 4096, K = 14336: M = 4 / 16 21.4 / 27.7 -> 13.6 / 19.2 us.
+// Measured (bf16, gs 64, rotating weight pool): K = 4096, N = 14336, M = 4 / 16
+// / 32: 11.2 / 12.4 / 17.3 us; N = 4096, K = 14336, M = 4 / 16 / 32: 11.6 /
+// 14.0 / 20.5 us (the round-1 kernel: 17.9 / 20.2 / 23.5 and 21.4 / 27.7 /
+// 39.8 us).
 #include <type_traits>
 
 #include "launch.h"
@@ -37,18 +43,62 @@
 namespace iqmm {
 namespace {
 
-template <int XT, int NT, int MT, int GB, int S, int D, int KB, bool GLU, bool MAPPED>
+__device__ __forceinline__ uint32_t lds_u32(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)(p)));
+}
+// one LDS DMA instruction: 16 bytes per lane from g to LDS byte m0 + 16 lane
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
+}
+__device__ __forceinline__ g_u32x4_t gload16(const void* g) {
+  g_u32x4_t v;
+  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(g) : "memory");
+  return v;
+}
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <int NT, int MT, int S, int D, bool XL>
+constexpr int dec_lds_bytes() {
+  constexpr int wave = D * (NT * 2048 + (XL ? MT * 8192 : 0));
+  constexpr int red = S > 1 ? S * NT * MT * 1024 : 0;
+  return S * wave > red ? S * wave : red;
+}
+
+// a configuration fits: LDS within 160 KiB, the loads of the stages in flight
+// behind the oldest within vmcnt's 6 bits
+template <int NT, int MT, int S, int D, bool XL>
+constexpr bool dec_fits() {
+  constexpr int per = 2 * NT + 8 * MT;
+  return dec_lds_bytes<NT, MT, S, D, XL>() <= 160 * 1024 && D <= 3 && (D - 1) * per < 64;
+}
+
+template <int XT, int NT, int MT, int GB, int S, int D, int KB, bool XL, bool GLU, bool MAPPED>
 __global__ __launch_bounds__(64 * S) void qmm_decode_kernel(QmmArgs a) {
   static_assert(!GLU || NT % 2 == 0, "GLU pairs gate tiles with up tiles");
+  static_assert(KB % 2 == 0, "stages of two blocks");
   constexpr int NC = GLU ? 8 * NT : 16 * NT;  // output columns per workgroup
   using XS = uint16_t;
   constexpr float CM = XT == BF16 ? 128.f : 1024.f;
   constexpr uint32_t EB = XT == BF16 ? 0x43434343u : 0x64646464u;
   constexpr uint32_t ONE2 = XT == BF16 ? 0x3f803f80u : 0x3c003c00u;
-  constexpr int JG = 4 / GB;         // MFMAs per group
-  constexpr int SH = KB * GB;        // 16-bit scale halves per row in the wave's K range
-  constexpr int SW = (SH + 1) / 2;   // 32-bit words holding them
-  __shared__ float red[S > 1 ? S * NT * MT * 256 : 1];
+  constexpr int JG = 4 / GB;            // MFMAs per group
+  constexpr int SW = (KB * GB + 1) / 2; // 32-bit scale words of the wave's K range
+  constexpr int NS = KB / 2;            // stages per wave
+  constexpr int WSTAGE = NT * 16 * 128; // weight bytes per stage
+  constexpr int XSTAGE = XL ? MT * 16 * 512 : 0;
+  constexpr int SSTAGE = WSTAGE + XSTAGE;
+  constexpr int WAVE_LDS = D * SSTAGE;
+  constexpr int LDS = dec_lds_bytes<NT, MT, S, D, XL>();
+  static_assert(LDS <= 160 * 1024, "LDS budget");
+  constexpr int NDW = 2 * NT;            // weight DMA instructions per stage (8 rows x 128 B)
+  constexpr int NDX = XL ? 8 * MT : 0;   // x DMA instructions per stage (2 rows x 512 B)
+  constexpr int NRX = XL ? 0 : 8 * MT;   // x register loads per stage (16 rows x 64 B)
+  constexpr int PER = NDW + NDX + NRX;   // vector-memory instructions per stage
+  __shared__ __attribute__((aligned(1024))) char lds[LDS];
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int M = a.M, N = a.N, K = a.K;
@@ -70,21 +120,41 @@ __global__ __launch_bounds__(64 * S) void qmm_decode_kernel(QmmArgs a) {
   const int r = lane & 15, q = lane >> 4;
   const int pb = KB * wave;  // first 128-code block of this wave
   const char* xbase = reinterpret_cast<const char*>(static_cast<const XS*>(a.x) + xb * a.x_mat);
-  const char* xr[MT];
-#pragma unroll
-  for (int i = 0; i < MT; ++i) xr[i] = xbase + min(i * 16 + r, M - 1) * xrow + pb * 256 + 16 * q;
   const char* w = reinterpret_cast<const char*>(a.w + wb * a.w_mat);
   const char* sp = reinterpret_cast<const char*>(static_cast<const XS*>(a.s) + wb * a.s_mat);
   const char* bp = reinterpret_cast<const char*>(static_cast<const XS*>(a.b) + wb * a.s_mat);
-  const char* wr[NT];
+  auto wrow_of = [&](int row) {  // tile row (0 .. 16 NT - 1) -> weight row
+    const int tt = row >> 4, rr = row & 15;
+    return GLU ? static_cast<int64_t>(tt / (NT / 2)) * N + min(n0 + 16 * (tt % (NT / 2)) + rr, N - 1)
+               : static_cast<int64_t>(min(n0 + row, N - 1));
+  };
+  // weight DMA u: tile rows 8u .. 8u + 7, lane -> row 8u + lane / 8, 16-byte
+  // position lane % 8 holding piece (lane % 8) ^ (row & 7) of the stage's 128 B
+  const char* wsrc[NDW];
+#pragma unroll
+  for (int u = 0; u < NDW; ++u) {
+    const int row = 8 * u + (lane >> 3);
+    wsrc[u] = w + wrow_of(row) * wrow + pb * 64 + 16 * ((lane & 7) ^ (row & 7));
+  }
+  // x DMA u (XL): rows 2u, 2u + 1, position lane % 32 holding piece
+  // (lane % 32) ^ (row & 15) of the row's 512-byte stage segment
+  const char* xsrc[XL ? NDX : 1];
+  const char* xr[XL ? 1 : MT];
+  if constexpr (XL) {
+#pragma unroll
+    for (int u = 0; u < NDX; ++u) {
+      const int row = 2 * u + (lane >> 5);
+      xsrc[u] = xbase + min(row, M - 1) * xrow + pb * 256 + 16 * ((lane & 31) ^ (row & 15));
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < MT; ++i) xr[i] = xbase + min(i * 16 + r, M - 1) * xrow + pb * 256 + 16 * q;
+  }
   uint32_t sw[NT][SW], bw[NT][SW];
 #pragma unroll
   for (int tt = 0; tt < NT; ++tt) {
-    const int64_t n = GLU ? static_cast<int64_t>(tt / (NT / 2)) * N + min(n0 + 16 * (tt % (NT / 2)) + r, N - 1)
-                          : min(n0 + 16 * tt + r, N - 1);
-    wr[tt] = w + n * wrow + pb * 64 + 16 * q;
-    // the scale halves of [pb, pb + KB) start at half pb * GB; pb * GB is even
-    // unless GB = 1 and KB is odd, which the launcher excludes
+    const int64_t n = wrow_of(16 * tt + r);
+    // the scale halves of [pb, pb + KB) start at half pb * GB (even: KB is even)
     const char* s0 = sp + n * srow + pb * GB * 2;
     const char* b0 = bp + n * srow + pb * GB * 2;
 #pragma unroll
@@ -93,18 +163,25 @@ __global__ __launch_bounds__(64 * S) void qmm_decode_kernel(QmmArgs a) {
       bw[tt][h] = *reinterpret_cast<const uint32_t*>(b0 + 4 * h);
     }
   }
-  struct Blk {
-    g_u32x4_t xa[MT][4];
-    g_u32x4_t wv[NT];
-  };
-  auto load = [&](int b, Blk& B) {
+  // the compiler sees this wait: nothing of its own is outstanding in the K loop
+  __builtin_amdgcn_s_waitcnt(0);
+  const uint32_t lds_wave = __builtin_amdgcn_readfirstlane(lds_u32(lds)) + wave * WAVE_LDS;
+  const char* lds_w = lds + wave * WAVE_LDS;
+  g_u32x4_t xreg[XL ? 1 : D][2][MT][4];
+  auto issue = [&](int st, int slot) {  // stage st (blocks 2 st, 2 st + 1) into ring slot
 #pragma unroll
-    for (int i = 0; i < MT; ++i)
+    for (int u = 0; u < NDW; ++u) dma16(wsrc[u] + st * 128, lds_wave + slot * SSTAGE + u * 1024);
+    if constexpr (XL) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) B.xa[i][j] = *reinterpret_cast<const g_u32x4_t*>(xr[i] + b * 256 + 64 * j);
+      for (int u = 0; u < NDX; ++u) dma16(xsrc[u] + st * 512, lds_wave + slot * SSTAGE + WSTAGE + u * 1024);
+    } else {
 #pragma unroll
-    for (int tt = 0; tt < NT; ++tt)
-      B.wv[tt] = __builtin_nontemporal_load(reinterpret_cast<const g_u32x4_t*>(wr[tt] + b * 64));
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) xreg[slot][h][i][j] = gload16(xr[i] + (2 * st + h) * 256 + 64 * j);
+    }
   };
   f32x4d_t Y[NT][MT];
 #pragma unroll
@@ -112,14 +189,20 @@ __global__ __launch_bounds__(64 * S) void qmm_decode_kernel(QmmArgs a) {
 #pragma unroll
     for (int i = 0; i < MT; ++i) Y[tt][i] = f32x4d_t{0.f, 0.f, 0.f, 0.f};
   const g_u32x4_t ones = {ONE2, ONE2, ONE2, ONE2};
-  auto compute = [&](const Blk& B, int b) {
+  auto compute = [&](int slot, int h, int b) {  // block b (half h of the stage in `slot`)
     g_u32x4_t A[MT][4];
 #pragma unroll
     for (int i = 0; i < MT; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
+        g_u32x4_t v;
+        if constexpr (XL) {
+          const int m = 16 * i + r, p = 16 * h + 4 * j + q;  // 16-byte piece of the row's stage segment
+          v = *reinterpret_cast<const g_u32x4_t*>(lds_w + slot * SSTAGE + WSTAGE + m * 512 + 16 * (p ^ (m & 15)));
+        } else {
+          v = xreg[slot][h][i][j];
+        }
         // (x0,x4) (x1,x5) (x2,x6) (x3,x7), the pair order of the weights below
-        const g_u32x4_t v = B.xa[i][j];
         A[i][j] = g_u32x4_t{__builtin_amdgcn_perm(v.z, v.x, 0x05040100u), __builtin_amdgcn_perm(v.z, v.x, 0x07060302u),
                             __builtin_amdgcn_perm(v.w, v.y, 0x05040100u), __builtin_amdgcn_perm(v.w, v.y, 0x07060302u)};
       }
@@ -134,9 +217,12 @@ __global__ __launch_bounds__(64 * S) void qmm_decode_kernel(QmmArgs a) {
       }
 #pragma unroll
     for (int tt = 0; tt < NT; ++tt) {
-      uint32_t wd[4] = {B.wv[tt].x, B.wv[tt].y, B.wv[tt].z, B.wv[tt].w};
+      const int row = 16 * tt + r;
+      const g_u32x4_t wv =
+          *reinterpret_cast<const g_u32x4_t*>(lds_w + slot * SSTAGE + row * 128 + 16 * ((4 * h + q) ^ (row & 7)));
+      uint32_t wd[4] = {wv.x, wv.y, wv.z, wv.w};
       // 4 x 4 transpose over the lanes q: afterwards wd[j] of lane q is dword
-      // q of the chunk that lane j loaded (chunk 4p + j)
+      // q of chunk 4p + j
       auto s02 = __builtin_amdgcn_permlane32_swap(wd[0], wd[2], false, false);
       auto s13 = __builtin_amdgcn_permlane32_swap(wd[1], wd[3], false, false);
       auto s01 = __builtin_amdgcn_permlane16_swap(s02[0], s13[0], false, false);
@@ -166,13 +252,33 @@ __global__ __launch_bounds__(64 * S) void qmm_decode_kernel(QmmArgs a) {
       }
     }
   };
-  Blk ring[D];
 #pragma unroll
-  for (int d = 0; d < D && d < KB; ++d) load(d, ring[d]);
+  for (int st = 0; st < D && st < NS; ++st) issue(st, st);
 #pragma unroll
-  for (int b = 0; b < KB; ++b) {
-    compute(ring[b % D], b);
-    if (b + D < KB) load(b + D, ring[b % D]);
+  for (int st = 0; st < NS; ++st) {
+    const int slot = st % D;
+    // stage st complete; the later stages issued so far (PER instructions
+    // each) may stay in flight
+    const int later = st + D <= NS ? D - 1 : NS - 1 - st;
+    static_assert(D <= 3 && (D - 1) * PER < 64, "vmcnt holds at most 63 outstanding loads");
+    if (later == 2) vm_wait<(D >= 3 ? 2 * PER : 0)>();
+    else if (later == 1) vm_wait<PER>();
+    else vm_wait<0>();
+    if constexpr (!XL) {
+      // the stage's x registers are written by the loads the wait covered
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) asm volatile("" : "+v"(xreg[slot][h][i][j])::"memory");
+    }
+    compute(slot, 0, 2 * st);
+    compute(slot, 1, 2 * st + 1);
+    if (st + D < NS) {
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the slot's LDS reads are done
+      issue(st + D, slot);
+    }
   }
   // lane holds Y[m = 16 i + 4 q + v][n = 16 tt + r] of each tile
   if constexpr (S == 1) {
@@ -189,6 +295,8 @@ __global__ __launch_bounds__(64 * S) void qmm_decode_kernel(QmmArgs a) {
         }
     return;
   }
+  __syncthreads();  // every wave's ring reads are done before the partials overwrite LDS
+  float* red = reinterpret_cast<float*>(lds);
 #pragma unroll
   for (int tt = 0; tt < NT; ++tt)
 #pragma unroll
@@ -203,10 +311,10 @@ __global__ __launch_bounds__(64 * S) void qmm_decode_kernel(QmmArgs a) {
     if constexpr (GLU) {
       float acc[2] = {0.f, 0.f};
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int tt = h * (NT / 2) + (nn >> 4);
+      for (int hh = 0; hh < 2; ++hh) {
+        const int tt = hh * (NT / 2) + (nn >> 4);
 #pragma unroll
-        for (int w2 = 0; w2 < S; ++w2) acc[h] += red[((w2 * NT + tt) * MT + i) * 256 + mr * 16 + (nn & 15)];
+        for (int w2 = 0; w2 < S; ++w2) acc[hh] += red[((w2 * NT + tt) * MT + i) * 256 + mr * 16 + (nn & 15)];
       }
       out[static_cast<int64_t>(m) * N + n0 + nn] = swiglu_out<XT>(acc[0], acc[1]);
     } else {
@@ -219,84 +327,73 @@ __global__ __launch_bounds__(64 * S) void qmm_decode_kernel(QmmArgs a) {
   }
 }
 
-// One configuration: NT tiles per workgroup, MT x-row tiles, S waves, D
-// blocks in flight, KB blocks per wave (K = 128 KB S).
+// One configuration: NT tiles per workgroup, S waves, D stages in flight, KB
+// blocks per wave (K = 128 KB S), XL: x through the LDS ring.
 struct DecCfg {
   int nt, s, d, kb;
+  bool xl;
 };
 
-// Choice per shape (measured on MI355X, bf16, gs 64, M in {4, 8, 16, 32}):
-// wide matrices (>= 8192 rows) take four tiles and eight waves of four
-// blocks (K = 4096); 6144 rows two tiles; narrower ones one tile and four
-// waves of eight blocks so that enough workgroups exist; K = 14336 four waves
-// of 28 blocks (M <= 16) or eight of 14 (M > 16).
+// Choice per shape, measured on MI355X (bf16, gs 64, M in {4, 8, 16, 32},
+// rotating weight pool): K = 4096 with >= 8192 rows: four tiles, eight waves,
+// x in registers (four tiles share each x fragment); 6144 rows: two tiles, x
+// in registers up to M = 8, through LDS above; narrower matrices and K = 14336:
+// one tile, four waves, x through LDS (down projection M = 16: 19.2 -> 14.0 us).
 DecCfg choose(const QmmArgs& a, int64_t rows) {
   const int P = a.K >> 7;
   const bool two_mt = a.M > 16;
-  DecCfg c{1, 4, 3, 0};
-  if (P == 32) {
-    if (rows >= 8192) c = DecCfg{4, 8, 2, 4};
-    else if (rows >= 6144) c = DecCfg{2, 8, 2, 4};
-    else c = two_mt ? DecCfg{1, 8, 2, 4} : DecCfg{1, 4, 3, 8};
-  } else if (P == 112) {
-    c = two_mt ? DecCfg{1, 8, 2, 14} : DecCfg{1, 4, 3, 28};
-  } else if (P % 8 == 0 && P / 8 <= 32) {
-    c = DecCfg{1, 8, 2, P / 8};
-  } else if (P % 4 == 0 && P / 4 <= 32) {
-    c = DecCfg{1, 4, 3, P / 4};
-  } else {
-    c.kb = 0;  // unsupported
+  DecCfg c{0, 0, 0, 0, false};
+  if (P == 32 && rows >= 8192) c = DecCfg{4, 8, 2, 4, false};
+  else if (P == 32 && rows >= 6144) c = a.M <= 8 ? DecCfg{2, 8, 2, 4, false} : DecCfg{2, 4, 2, 8, true};
+  else if (P == 8 || P == 16 || P == 32 || P == 64 || P == 112) c = DecCfg{1, 4, two_mt ? 2 : 3, P / 4, true};
+  if (a.glu && c.nt == 1) {
+    c.nt = 2;
+    c.d = 2;  // two tiles of x + weights in the LDS budget
   }
-  if (a.glu && c.nt < 2) c.nt = 2;
   return c;
 }
 
-template <int XT, int NT, int MT, int GB, int S, int D, int KB, bool GLU>
+template <int XT, int NT, int MT, int GB, int S, int D, int KB, bool XL, bool GLU>
 hipError_t dec_go(const QmmArgs& a, dim3 grid) {
-  if constexpr (GLU && NT % 2 != 0) {
-    return hipErrorInvalidValue;  // choose() gives GLU two or more tiles
+  if constexpr ((GLU && NT % 2 != 0) || !dec_fits<NT, MT, S, D, XL>()) {
+    return hipErrorInvalidValue;  // not produced by choose()
   } else {
-  const bool mapped = a.bm.ndim != 0 || a.bm.lhs != nullptr || a.bm.rhs != nullptr;
-  if (mapped)
-    hipLaunchKernelGGL((qmm_decode_kernel<XT, NT, MT, GB, S, D, KB, GLU, true>), grid, dim3(64 * S), 0, a.stream, a);
-  else
-    hipLaunchKernelGGL((qmm_decode_kernel<XT, NT, MT, GB, S, D, KB, GLU, false>), grid, dim3(64 * S), 0, a.stream, a);
-  return hipGetLastError();
+    const bool mapped = a.bm.ndim != 0 || a.bm.lhs != nullptr || a.bm.rhs != nullptr;
+    if (mapped)
+      hipLaunchKernelGGL((qmm_decode_kernel<XT, NT, MT, GB, S, D, KB, XL, GLU, true>), grid, dim3(64 * S), 0,
+                         a.stream, a);
+    else
+      hipLaunchKernelGGL((qmm_decode_kernel<XT, NT, MT, GB, S, D, KB, XL, GLU, false>), grid, dim3(64 * S), 0,
+                         a.stream, a);
+    return hipGetLastError();
   }
 }
 
-// the instantiated (NT, S, D, KB) configurations
+// the configurations choose() produces
+#define IQMM_DEC_CONFIGS(X)                                                                           \
+  X(4, 8, 2, 4, false) X(2, 8, 2, 4, false) X(2, 4, 2, 8, true) X(1, 4, 3, 2, true) X(1, 4, 2, 2, true) \
+  X(1, 4, 3, 4, true) X(1, 4, 2, 4, true) X(1, 4, 3, 8, true) X(1, 4, 2, 8, true) X(1, 4, 3, 16, true) \
+  X(1, 4, 2, 16, true) X(1, 4, 3, 28, true) X(1, 4, 2, 28, true) X(2, 4, 2, 2, true)                  \
+  X(2, 4, 2, 4, true) X(2, 4, 2, 16, true) X(2, 4, 2, 28, true)
+
 template <int XT, int MT, int GB, bool GLU>
 hipError_t dec_cfg(const QmmArgs& a, const DecCfg& c, dim3 grid) {
-#define IQMM_DEC(NT_, S_, D_, KB_)                                                    \
-  if (c.nt == NT_ && c.s == S_ && c.d == D_ && c.kb == KB_)                           \
-    return dec_go<XT, NT_, MT, GB, S_, D_, KB_, GLU>(a, grid);
-  IQMM_DEC(4, 8, 2, 4)
-  IQMM_DEC(2, 8, 2, 4)
-  IQMM_DEC(1, 8, 2, 4)
-  IQMM_DEC(1, 4, 3, 8)
-  IQMM_DEC(2, 4, 3, 8)
-  IQMM_DEC(1, 8, 2, 14)
-  IQMM_DEC(2, 8, 2, 14)
-  IQMM_DEC(1, 4, 3, 28)
-  IQMM_DEC(2, 4, 3, 28)
-  IQMM_DEC(1, 8, 2, 8)
-  IQMM_DEC(2, 8, 2, 8)
-  IQMM_DEC(1, 8, 2, 2)
-  IQMM_DEC(2, 8, 2, 2)
-  IQMM_DEC(1, 8, 2, 16)
-  IQMM_DEC(2, 8, 2, 16)
+#define IQMM_DEC(NT_, S_, D_, KB_, XL_)                                              \
+  if (c.nt == NT_ && c.s == S_ && c.d == D_ && c.kb == KB_ && c.xl == XL_)          \
+    return dec_go<XT, NT_, MT, GB, S_, D_, KB_, XL_, GLU>(a, grid);
+  IQMM_DEC_CONFIGS(IQMM_DEC)
 #undef IQMM_DEC
   return hipErrorInvalidValue;
 }
 
-bool cfg_instantiated(const DecCfg& c) {
-  static const DecCfg known[] = {{4, 8, 2, 4}, {2, 8, 2, 4}, {1, 8, 2, 4}, {1, 4, 3, 8}, {2, 4, 3, 8},
-                                 {1, 8, 2, 14}, {2, 8, 2, 14}, {1, 4, 3, 28}, {2, 4, 3, 28}, {1, 8, 2, 8},
-                                 {2, 8, 2, 8}, {1, 8, 2, 2}, {2, 8, 2, 2}, {1, 8, 2, 16}, {2, 8, 2, 16}};
-  for (const DecCfg& k : known)
-    if (k.nt == c.nt && k.s == c.s && k.d == c.d && k.kb == c.kb) return true;
-  return false;
+bool cfg_instantiated(const DecCfg& c, int mt) {
+  bool ok = false;
+#define IQMM_DEC_K(NT_, S_, D_, KB_, XL_)                                                              \
+  ok = ok || (c.nt == NT_ && c.s == S_ && c.d == D_ && c.kb == KB_ && c.xl == XL_ &&                    \
+              (mt == 1 ? dec_fits<NT_, 1, S_, D_, XL_>() : dec_fits<NT_, 2, S_, D_, XL_>()));
+  IQMM_DEC_CONFIGS(IQMM_DEC_K)
+#undef IQMM_DEC_K
+  return ok;
 }
 
 template <int XT, int GB, bool GLU>
@@ -326,9 +423,7 @@ bool qmm_decode_supported(const QmmArgs& a) {
   if (a.gs != 32 && a.gs != 64 && a.gs != 128) return false;
   const int64_t rows = static_cast<int64_t>(a.N) * (a.glu ? 2 : 1) * a.nbatch;
   const DecCfg c = choose(a, rows);
-  if (c.kb == 0 || c.kb * c.s * 128 != a.K || !cfg_instantiated(c)) return false;
-  // gs 128: one scale half per block, the wave's first half must start a word
-  if (a.gs == 128 && c.kb % 2 != 0) return false;
+  if (c.kb == 0 || c.kb * c.s * 128 != a.K || !cfg_instantiated(c, a.M > 16 ? 2 : 1)) return false;
   // scales / biases are read as aligned 32-bit words
   const bool aligned = (reinterpret_cast<uintptr_t>(a.s) | reinterpret_cast<uintptr_t>(a.b)) % 4 == 0 &&
                        ((a.K / a.gs) * 2) % 4 == 0;
