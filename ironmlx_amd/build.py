@@ -8,6 +8,7 @@ from __future__ import annotations
 
 import concurrent.futures as cf
 import os
+import re
 import subprocess
 import sys
 
@@ -26,12 +27,38 @@ FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
          "-Wno-unused-result"]
 
 
+# Kernels whose K loops load into registers with inline assembly and wait with
+# explicit vmcnt: the compiler treats such an output as written when the asm
+# statement issues, so a kernel that spills (or otherwise moves a register
+# before its load has landed) would read stale data or have a late load
+# overwrite a register reused meanwhile.  Their files are compiled with the
+# resource-usage report and the build fails if any kernel uses scratch.
+NO_SCRATCH = {"qmm_decode.hip", "qmm_gather.hip"}
+
+
+def scratch_kernels(remarks: str) -> list[str]:
+    """Kernels of a -Rpass-analysis=kernel-resource-usage report with scratch."""
+    out = []
+    for block in remarks.split("remark: Function Name: ")[1:]:
+        name = block.split()[0]
+        m = re.search(r"ScratchSize \[bytes/lane\]: (\d+)", block)
+        if m and int(m.group(1)) > 0:
+            out.append(name)
+    return out
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(OBJ, os.path.splitext(src)[0] + ".o")
-    cmd = [HIPCC, *FLAGS, *FILE_FLAGS.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
+    extra = ["-Rpass-analysis=kernel-resource-usage"] if src in NO_SCRATCH else []
+    cmd = [HIPCC, *FLAGS, *FILE_FLAGS.get(src, []), *extra, "-c", os.path.join(CSRC, src), "-o", obj]
     p = subprocess.run(cmd, capture_output=True, text=True)
     if p.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{p.stderr}")
+    if src in NO_SCRATCH:
+        bad = scratch_kernels(p.stderr)
+        if bad:
+            os.remove(obj)
+            raise RuntimeError(f"{src}: kernels with register loads in flight use scratch: {bad[:8]}")
     return obj
 
 

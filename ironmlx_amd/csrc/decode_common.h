@@ -17,4 +17,97 @@ __device__ __forceinline__ f32x4d_t mfma16(const g_u32x4_t& a, const g_u32x4_t& 
                                                   __builtin_bit_cast(g_f16x8_t, b), c, 0, 0, 0);
 }
 
+__device__ __forceinline__ uint32_t lds_u32(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)(p)));
+}
+// one LDS DMA instruction: 16 bytes per lane from g to LDS byte m0 + 16 lane
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
+}
+// A register load whose completion the caller waits for with vm_wait: the
+// compiler takes the output as written when the statement issues, so a kernel
+// using it must not spill or move that register before the wait (the build
+// rejects such kernels that use scratch), and the caller ties the register to
+// its wait with an empty asm statement ("+v").
+__device__ __forceinline__ g_u32x4_t gload16(const void* g) {
+  g_u32x4_t v;
+  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(g) : "memory");
+  return v;
+}
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// x fragment (16 bytes: codes 8p .. 8p + 7 of one row) -> MFMA A operand in
+// the pair order (x0,x4) (x1,x5) (x2,x6) (x3,x7) of the unpacked weights
+__device__ __forceinline__ g_u32x4_t x_pairs(const g_u32x4_t& v) {
+  return g_u32x4_t{__builtin_amdgcn_perm(v.z, v.x, 0x05040100u), __builtin_amdgcn_perm(v.z, v.x, 0x07060302u),
+                   __builtin_amdgcn_perm(v.w, v.y, 0x05040100u), __builtin_amdgcn_perm(v.w, v.y, 0x07060302u)};
+}
+
+// One 128-code block of the factored affine 4-bit product for NT 16-row
+// weight tiles and MT 16-row x tiles.  A holds the x operands (x_pairs) of
+// the block's four 32-code MFMA slots; the weights are the block's 64-byte
+// row pieces in LDS at wst + row * 128 + 16 * ((4 h + q) ^ (row & 7)) (h: the
+// block's half of a two-block stage, pieces XOR-swizzled by the row); sw / bw
+// hold the scale / bias halves of the wave's K range, hb the first half of
+// this block.  Y[tt][i] accumulates sum_g s D + (b - C s) X.
+template <int XT, int NT, int MT, int GB, int SW>
+__device__ __forceinline__ void fac_block(f32x4d_t (&Y)[NT][MT], const g_u32x4_t (&A)[MT][4], const char* wst, int h,
+                                          int hb, const uint32_t (&sw)[NT][SW], const uint32_t (&bw)[NT][SW], int r,
+                                          int q) {
+  using XS = uint16_t;
+  constexpr float CM = XT == BF16 ? 128.f : 1024.f;
+  constexpr uint32_t EB = XT == BF16 ? 0x43434343u : 0x64646464u;
+  constexpr uint32_t ONE2 = XT == BF16 ? 0x3f803f80u : 0x3c003c00u;
+  constexpr int JG = 4 / GB;  // MFMAs per group
+  const g_u32x4_t ones = {ONE2, ONE2, ONE2, ONE2};
+  f32x4d_t XG[MT][GB];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int g = 0; g < GB; ++g) {
+      XG[i][g] = mfma16<XT>(A[i][g * JG], ones, f32x4d_t{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+      for (int j = 1; j < JG; ++j) XG[i][g] = mfma16<XT>(A[i][g * JG + j], ones, XG[i][g]);
+    }
+#pragma unroll
+  for (int tt = 0; tt < NT; ++tt) {
+    const int row = 16 * tt + r;
+    const g_u32x4_t wv = *reinterpret_cast<const g_u32x4_t*>(wst + row * 128 + 16 * ((4 * h + q) ^ (row & 7)));
+    uint32_t wd[4] = {wv.x, wv.y, wv.z, wv.w};
+    // 4 x 4 transpose over the lanes q: afterwards wd[j] of lane q is dword q
+    // of chunk 4p + j
+    auto s02 = __builtin_amdgcn_permlane32_swap(wd[0], wd[2], false, false);
+    auto s13 = __builtin_amdgcn_permlane32_swap(wd[1], wd[3], false, false);
+    auto s01 = __builtin_amdgcn_permlane16_swap(s02[0], s13[0], false, false);
+    auto s23 = __builtin_amdgcn_permlane16_swap(s02[1], s13[1], false, false);
+    wd[0] = s01[0]; wd[1] = s01[1]; wd[2] = s23[0]; wd[3] = s23[1];
+    g_u32x4_t Wp[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t lo = wd[j] & 0x0F0F0F0Fu, hi = (wd[j] >> 4) & 0x0F0F0F0Fu;
+      Wp[j] = g_u32x4_t{__builtin_amdgcn_perm(EB, lo, 0x04020400u), __builtin_amdgcn_perm(EB, hi, 0x04020400u),
+                        __builtin_amdgcn_perm(EB, lo, 0x04030401u), __builtin_amdgcn_perm(EB, hi, 0x04030401u)};
+    }
+#pragma unroll
+    for (int g = 0; g < GB; ++g) {
+      const int hf = hb + g;
+      const float s = to_f<XT>(static_cast<XS>(sw[tt][hf >> 1] >> (16 * (hf & 1))));
+      const float bs = to_f<XT>(static_cast<XS>(bw[tt][hf >> 1] >> (16 * (hf & 1))));
+      const float cb = fmaf(-CM, s, bs);
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        f32x4d_t Dd = mfma16<XT>(A[i][g * JG], Wp[g * JG], f32x4d_t{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+        for (int j = 1; j < JG; ++j) Dd = mfma16<XT>(A[i][g * JG + j], Wp[g * JG + j], Dd);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) Y[tt][i][v] = fmaf(s, Dd[v], fmaf(cb, XG[i][g][v], Y[tt][i][v]));
+      }
+    }
+  }
+}
+
 }  // namespace iqmm

@@ -43,37 +43,20 @@
 namespace iqmm {
 namespace {
 
-__device__ __forceinline__ uint32_t lds_u32(const void* p) {
-  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)(p)));
-}
-// one LDS DMA instruction: 16 bytes per lane from g to LDS byte m0 + 16 lane
-__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
-}
-__device__ __forceinline__ g_u32x4_t gload16(const void* g) {
-  g_u32x4_t v;
-  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(g) : "memory");
-  return v;
-}
-template <int N>
-__device__ __forceinline__ void vm_wait() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-template <int NT, int MT, int S, int D, bool XL>
+template <int NT, int MT, int S, int D, bool XL, int KB>
 constexpr int dec_lds_bytes() {
-  constexpr int wave = D * (NT * 2048 + (XL ? MT * 8192 : 0));
+  constexpr int ring = D < KB / 2 ? D : KB / 2;  // stages allocated
+  constexpr int wave = ring * (NT * 2048 + (XL ? MT * 8192 : 0));
   constexpr int red = S > 1 ? S * NT * MT * 1024 : 0;
   return S * wave > red ? S * wave : red;
 }
 
 // a configuration fits: LDS within 160 KiB, the loads of the stages in flight
 // behind the oldest within vmcnt's 6 bits
-template <int NT, int MT, int S, int D, bool XL>
+template <int NT, int MT, int S, int D, bool XL, int KB>
 constexpr bool dec_fits() {
   constexpr int per = 2 * NT + 8 * MT;
-  return dec_lds_bytes<NT, MT, S, D, XL>() <= 160 * 1024 && D <= 3 && (D - 1) * per < 64;
+  return dec_lds_bytes<NT, MT, S, D, XL, KB>() <= 160 * 1024 && D <= 3 && (D - 1) * per < 64;
 }
 
 template <int XT, int NT, int MT, int GB, int S, int D, int KB, bool XL, bool GLU, bool MAPPED>
@@ -82,17 +65,13 @@ __global__ __launch_bounds__(64 * S) void qmm_decode_kernel(QmmArgs a) {
   static_assert(KB % 2 == 0, "stages of two blocks");
   constexpr int NC = GLU ? 8 * NT : 16 * NT;  // output columns per workgroup
   using XS = uint16_t;
-  constexpr float CM = XT == BF16 ? 128.f : 1024.f;
-  constexpr uint32_t EB = XT == BF16 ? 0x43434343u : 0x64646464u;
-  constexpr uint32_t ONE2 = XT == BF16 ? 0x3f803f80u : 0x3c003c00u;
-  constexpr int JG = 4 / GB;            // MFMAs per group
   constexpr int SW = (KB * GB + 1) / 2; // 32-bit scale words of the wave's K range
   constexpr int NS = KB / 2;            // stages per wave
   constexpr int WSTAGE = NT * 16 * 128; // weight bytes per stage
   constexpr int XSTAGE = XL ? MT * 16 * 512 : 0;
   constexpr int SSTAGE = WSTAGE + XSTAGE;
-  constexpr int WAVE_LDS = D * SSTAGE;
-  constexpr int LDS = dec_lds_bytes<NT, MT, S, D, XL>();
+  constexpr int WAVE_LDS = (D < NS ? D : NS) * SSTAGE;
+  constexpr int LDS = dec_lds_bytes<NT, MT, S, D, XL, KB>();
   static_assert(LDS <= 160 * 1024, "LDS budget");
   constexpr int NDW = 2 * NT;            // weight DMA instructions per stage (8 rows x 128 B)
   constexpr int NDX = XL ? 8 * MT : 0;   // x DMA instructions per stage (2 rows x 512 B)
@@ -188,69 +167,21 @@ __global__ __launch_bounds__(64 * S) void qmm_decode_kernel(QmmArgs a) {
   for (int tt = 0; tt < NT; ++tt)
 #pragma unroll
     for (int i = 0; i < MT; ++i) Y[tt][i] = f32x4d_t{0.f, 0.f, 0.f, 0.f};
-  const g_u32x4_t ones = {ONE2, ONE2, ONE2, ONE2};
   auto compute = [&](int slot, int h, int b) {  // block b (half h of the stage in `slot`)
     g_u32x4_t A[MT][4];
 #pragma unroll
     for (int i = 0; i < MT; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        g_u32x4_t v;
         if constexpr (XL) {
           const int m = 16 * i + r, p = 16 * h + 4 * j + q;  // 16-byte piece of the row's stage segment
-          v = *reinterpret_cast<const g_u32x4_t*>(lds_w + slot * SSTAGE + WSTAGE + m * 512 + 16 * (p ^ (m & 15)));
+          A[i][j] = x_pairs(
+              *reinterpret_cast<const g_u32x4_t*>(lds_w + slot * SSTAGE + WSTAGE + m * 512 + 16 * (p ^ (m & 15))));
         } else {
-          v = xreg[slot][h][i][j];
-        }
-        // (x0,x4) (x1,x5) (x2,x6) (x3,x7), the pair order of the weights below
-        A[i][j] = g_u32x4_t{__builtin_amdgcn_perm(v.z, v.x, 0x05040100u), __builtin_amdgcn_perm(v.z, v.x, 0x07060302u),
-                            __builtin_amdgcn_perm(v.w, v.y, 0x05040100u), __builtin_amdgcn_perm(v.w, v.y, 0x07060302u)};
-      }
-    f32x4d_t XG[MT][GB];
-#pragma unroll
-    for (int i = 0; i < MT; ++i)
-#pragma unroll
-      for (int g = 0; g < GB; ++g) {
-        XG[i][g] = mfma16<XT>(A[i][g * JG], ones, f32x4d_t{0.f, 0.f, 0.f, 0.f});
-#pragma unroll
-        for (int j = 1; j < JG; ++j) XG[i][g] = mfma16<XT>(A[i][g * JG + j], ones, XG[i][g]);
-      }
-#pragma unroll
-    for (int tt = 0; tt < NT; ++tt) {
-      const int row = 16 * tt + r;
-      const g_u32x4_t wv =
-          *reinterpret_cast<const g_u32x4_t*>(lds_w + slot * SSTAGE + row * 128 + 16 * ((4 * h + q) ^ (row & 7)));
-      uint32_t wd[4] = {wv.x, wv.y, wv.z, wv.w};
-      // 4 x 4 transpose over the lanes q: afterwards wd[j] of lane q is dword
-      // q of chunk 4p + j
-      auto s02 = __builtin_amdgcn_permlane32_swap(wd[0], wd[2], false, false);
-      auto s13 = __builtin_amdgcn_permlane32_swap(wd[1], wd[3], false, false);
-      auto s01 = __builtin_amdgcn_permlane16_swap(s02[0], s13[0], false, false);
-      auto s23 = __builtin_amdgcn_permlane16_swap(s02[1], s13[1], false, false);
-      wd[0] = s01[0]; wd[1] = s01[1]; wd[2] = s23[0]; wd[3] = s23[1];
-      g_u32x4_t Wp[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t lo = wd[j] & 0x0F0F0F0Fu, hi = (wd[j] >> 4) & 0x0F0F0F0Fu;
-        Wp[j] = g_u32x4_t{__builtin_amdgcn_perm(EB, lo, 0x04020400u), __builtin_amdgcn_perm(EB, hi, 0x04020400u),
-                          __builtin_amdgcn_perm(EB, lo, 0x04030401u), __builtin_amdgcn_perm(EB, hi, 0x04030401u)};
-      }
-#pragma unroll
-      for (int g = 0; g < GB; ++g) {
-        const int hf = b * GB + g;  // scale half of this group within the range
-        const float s = to_f<XT>(static_cast<XS>(sw[tt][hf >> 1] >> (16 * (hf & 1))));
-        const float bs = to_f<XT>(static_cast<XS>(bw[tt][hf >> 1] >> (16 * (hf & 1))));
-        const float cb = fmaf(-CM, s, bs);
-#pragma unroll
-        for (int i = 0; i < MT; ++i) {
-          f32x4d_t Dd = mfma16<XT>(A[i][g * JG], Wp[g * JG], f32x4d_t{0.f, 0.f, 0.f, 0.f});
-#pragma unroll
-          for (int j = 1; j < JG; ++j) Dd = mfma16<XT>(A[i][g * JG + j], Wp[g * JG + j], Dd);
-#pragma unroll
-          for (int v = 0; v < 4; ++v) Y[tt][i][v] = fmaf(s, Dd[v], fmaf(cb, XG[i][g][v], Y[tt][i][v]));
+          A[i][j] = x_pairs(xreg[slot][h][i][j]);
         }
       }
-    }
+    fac_block<XT, NT, MT, GB, SW>(Y, A, lds_w + slot * SSTAGE, h, b * GB, sw, bw, r, q);
   };
 #pragma unroll
   for (int st = 0; st < D && st < NS; ++st) issue(st, st);
@@ -346,6 +277,9 @@ DecCfg choose(const QmmArgs& a, int64_t rows) {
   if (P == 32 && rows >= 8192) c = DecCfg{4, 8, 2, 4, false};
   else if (P == 32 && rows >= 6144) c = a.M <= 8 ? DecCfg{2, 8, 2, 4, false} : DecCfg{2, 4, 2, 8, true};
   else if (P == 8 || P == 16 || P == 32 || P == 64 || P == 112) c = DecCfg{1, 4, two_mt ? 2 : 3, P / 4, true};
+  // gs 32 at two m tiles: four tiles' scale words do not fit in registers
+  // next to the x ring
+  if (a.gs == 32 && two_mt && c.nt == 4 && !c.xl) c.nt = 2;
   if (a.glu && c.nt == 1) {
     c.nt = 2;
     c.d = 2;  // two tiles of x + weights in the LDS budget
@@ -355,7 +289,7 @@ DecCfg choose(const QmmArgs& a, int64_t rows) {
 
 template <int XT, int NT, int MT, int GB, int S, int D, int KB, bool XL, bool GLU>
 hipError_t dec_go(const QmmArgs& a, dim3 grid) {
-  if constexpr ((GLU && NT % 2 != 0) || !dec_fits<NT, MT, S, D, XL>()) {
+  if constexpr ((GLU && NT % 2 != 0) || !dec_fits<NT, MT, S, D, XL, KB>() || (!XL && GB == 4 && NT == 4 && MT == 2)) {
     return hipErrorInvalidValue;  // not produced by choose()
   } else {
     const bool mapped = a.bm.ndim != 0 || a.bm.lhs != nullptr || a.bm.rhs != nullptr;
@@ -390,7 +324,7 @@ bool cfg_instantiated(const DecCfg& c, int mt) {
   bool ok = false;
 #define IQMM_DEC_K(NT_, S_, D_, KB_, XL_)                                                              \
   ok = ok || (c.nt == NT_ && c.s == S_ && c.d == D_ && c.kb == KB_ && c.xl == XL_ &&                    \
-              (mt == 1 ? dec_fits<NT_, 1, S_, D_, XL_>() : dec_fits<NT_, 2, S_, D_, XL_>()));
+              (mt == 1 ? dec_fits<NT_, 1, S_, D_, XL_, KB_>() : dec_fits<NT_, 2, S_, D_, XL_, KB_>()));
   IQMM_DEC_CONFIGS(IQMM_DEC_K)
 #undef IQMM_DEC_K
   return ok;

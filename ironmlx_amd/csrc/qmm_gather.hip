@@ -11,30 +11,61 @@ namespace {
 
 // Sorted grouped gather_qmm (sorted_indices; the MoE layer of
 // mlx/src/nn/moe.rs:84-170 over the stacked experts of
-// mlx/src/model/qwen35.rs:653-775) with the factored arithmetic above.
-// Workgroup (column block, expert e) takes the expert's rows [off[e],
-// off[e + 1]) of the flattened batch (x rows gathered through lhs), in passes
-// of up to 32 rows; each wave streams its K range of the expert's weight rows
-// per pass (the first pass from HBM, later ones from L2).  The scale / bias
-// words of the wave's range are read once.  Rows whose lhs index is out of
+// mlx/src/model/qwen35.rs:653-775) with the factored arithmetic of
+// qmm_decode.hip.  Workgroup (column block, expert e) takes the expert's rows
+// [off[e], off[e + 1]) of the flattened batch (x rows gathered through lhs),
+// in passes of up to 16 MTMAX rows.  Its S waves split K; each wave streams
+// its KB blocks of the NT weight tiles through its own LDS ring by LDS DMA
+// (8 rows x 128 B per instruction, as in qmm_decode.hip) with D stages of two
+// blocks in flight, and x straight into registers (16 rows x 64 B), or, with
+// XL, also through the ring (2 rows x 512 B).  The scale / bias words of the
+// wave's range are read once for every pass.  Rows whose lhs index is out of
 // range are written as NaN; workgroup e = E (one past the experts) writes NaN
 // for batch entries outside every expert's segment.
-template <int XT, int NT, int GB, int S, int D, int KB, bool GLU>
+template <int NT, int MT, int S, int D, bool XL, int KB>
+constexpr int gat_lds_bytes() {
+  constexpr int ring = D < KB / 2 ? D : KB / 2;  // stages allocated
+  constexpr int wave = ring * (NT * 2048 + (XL ? MT * 8192 : 0));
+  constexpr int red = S > 1 ? S * NT * MT * 1024 : 0;
+  return S * wave > red ? S * wave : red;
+}
+template <int NT, int MT, int S, int D, bool XL, int KB>
+constexpr bool gat_fits() {
+  return gat_lds_bytes<NT, MT, S, D, XL, KB>() <= 160 * 1024 && D <= 3 && (D - 1) * (2 * NT + 8 * MT) < 64;
+}
+
+template <int XT, int NT, int GB, int S, int D, int KB, bool XL, bool GLU, int MTMAX>
 __global__ __launch_bounds__(64 * S) void gather_decode_kernel(QmmArgs a, int64_t nflat, const int64_t* off) {
   static_assert(!GLU || NT % 2 == 0, "GLU pairs gate tiles with up tiles");
+  static_assert(KB % 2 == 0, "stages of two blocks");
   constexpr int NC = GLU ? 8 * NT : 16 * NT;
   using XS = uint16_t;
-  constexpr float CM = XT == BF16 ? 128.f : 1024.f;
-  constexpr uint32_t EB = XT == BF16 ? 0x43434343u : 0x64646464u;
-  constexpr uint32_t ONE2 = XT == BF16 ? 0x3f803f80u : 0x3c003c00u;
-  constexpr int JG = 4 / GB;
   constexpr int SW = (KB * GB + 1) / 2;
-  __shared__ float red[S > 1 ? S * NT * 2 * 256 : 1];
+  constexpr int NS = KB / 2;
+  constexpr int WSTAGE = NT * 16 * 128;
+  constexpr int XSTAGE = XL ? MTMAX * 16 * 512 : 0;
+  constexpr int SSTAGE = WSTAGE + XSTAGE;
+  constexpr int WAVE_LDS = (D < NS ? D : NS) * SSTAGE;
+  constexpr int LDS = gat_lds_bytes<NT, MTMAX, S, D, XL, KB>();
+  static_assert(gat_fits<NT, MTMAX, S, D, XL, KB>(), "LDS / vmcnt budget");
+  constexpr int NDW = 2 * NT;
+  __shared__ __attribute__((aligned(1024))) char lds[LDS];
+  // per pass row: element offset of its x row, and of its output row (one's
+  // complement when the row's lhs index is out of range: written as NaN)
+  __shared__ int64_t prow_x[16 * MTMAX], prow_o[16 * MTMAX];
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int Mx = a.M, N = a.N, K = a.K;
-  const int n0 = blockIdx.x * NC;
-  const int64_t e = blockIdx.y;
+  // one-dimensional grid of gx (E + 1) workgroups (E = a.bm.nw), dispatched
+  // round robin over the 8 XCDs (workgroup L on XCD L % 8); renumbered so that
+  // each XCD takes a contiguous range of (expert, column block) pairs and the
+  // column blocks of one expert share their gathered x rows in one L2
+  const int gx = (N + NC - 1) / NC;
+  const int64_t total = gridDim.x;
+  const int64_t L = blockIdx.x, per = total / 8;
+  const int64_t F = L < 8 * per ? (L % 8) * per + L / 8 : L;
+  const int n0 = static_cast<int>(F % gx) * NC;
+  const int64_t e = F / gx;
   XS* out = static_cast<XS*>(a.out);
   if (e == a.bm.nw) {
     // offsets are clamped into [0, nflat]: indices that are not sorted as
@@ -62,13 +93,21 @@ __global__ __launch_bounds__(64 * S) void gather_decode_kernel(QmmArgs a, int64_
   const char* w = reinterpret_cast<const char*>(a.w + e * a.w_mat);
   const char* sp = reinterpret_cast<const char*>(static_cast<const XS*>(a.s) + e * a.s_mat);
   const char* bp = reinterpret_cast<const char*>(static_cast<const XS*>(a.b) + e * a.s_mat);
-  const char* wr[NT];
+  auto wrow_of = [&](int row) {
+    const int tt = row >> 4, rr = row & 15;
+    return GLU ? static_cast<int64_t>(tt / (NT / 2)) * N + min(n0 + 16 * (tt % (NT / 2)) + rr, N - 1)
+               : static_cast<int64_t>(min(n0 + row, N - 1));
+  };
+  const char* wsrc[NDW];
+#pragma unroll
+  for (int u = 0; u < NDW; ++u) {
+    const int row = 8 * u + (lane >> 3);
+    wsrc[u] = w + wrow_of(row) * wrow + pb * 64 + 16 * ((lane & 7) ^ (row & 7));
+  }
   uint32_t sw[NT][SW], bw[NT][SW];
 #pragma unroll
   for (int tt = 0; tt < NT; ++tt) {
-    const int64_t n = GLU ? static_cast<int64_t>(tt / (NT / 2)) * N + min(n0 + 16 * (tt % (NT / 2)) + r, N - 1)
-                          : min(n0 + 16 * tt + r, N - 1);
-    wr[tt] = w + n * wrow + pb * 64 + 16 * q;
+    const int64_t n = wrow_of(16 * tt + r);
     const char* s0 = sp + n * srow + pb * GB * 2;
     const char* b0 = bp + n * srow + pb * GB * 2;
 #pragma unroll
@@ -77,103 +116,107 @@ __global__ __launch_bounds__(64 * S) void gather_decode_kernel(QmmArgs a, int64_
       bw[tt][h] = *reinterpret_cast<const uint32_t*>(b0 + 4 * h);
     }
   }
-  const g_u32x4_t ones = {ONE2, ONE2, ONE2, ONE2};
-  // one pass over rows [r0, r0 + 16 MT) of the expert
+  const uint32_t lds_wave = __builtin_amdgcn_readfirstlane(lds_u32(lds)) + wave * WAVE_LDS;
+  const char* lds_w = lds + wave * WAVE_LDS;
   auto pass = [&](auto mt_c, int64_t r0) {
     constexpr int MT = decltype(mt_c)::value;
-    const char* xr[MT];
-#pragma unroll
-    for (int i = 0; i < MT; ++i) {
-      const int64_t rr = min(r0 + 16 * i + r, rows_total - 1);
+    // rows past the segment repeat its last row; their outputs are not stored
+    if (t < 16 * MT) {
+      const int64_t rr = min(r0 + t, rows_total - 1);
       const int64_t b = blo + rr / Mx, mrow = rr % Mx;
       const int64_t xm = a.bm.lhs ? load_index(a.bm.lhs, a.bm.lhs_dt, b) : b;
-      const int64_t xs = (xm >= 0 && xm < a.bm.nx) ? xm : 0;
-      xr[i] = reinterpret_cast<const char*>(x + xs * a.x_mat + mrow * K) + pb * 256 + 16 * q;
+      const bool ok = xm >= 0 && xm < a.bm.nx;
+      prow_x[t] = (ok ? xm : 0) * a.x_mat + mrow * K;
+      prow_o[t] = ok ? (b * Mx + mrow) * N : ~((b * Mx + mrow) * N);
     }
-    struct Blk {
-      g_u32x4_t xa[MT][4];
-      g_u32x4_t wv[NT];
-    };
-    auto load = [&](int b, Blk& B) {
+    __syncthreads();
+    auto xrow_ptr = [&](int64_t, int m) { return reinterpret_cast<const char*>(x + prow_x[m]); };
+    constexpr int NDX = XL ? 8 * MT : 0;
+    constexpr int NRX = XL ? 0 : 8 * MT;
+    constexpr int PER = NDW + NDX + NRX;
+    static_assert((D - 1) * PER < 64, "vmcnt range");
+    const char* xsrc[XL ? NDX : 1];
+    const char* xr[XL ? 1 : MT];
+    if constexpr (XL) {
 #pragma unroll
-      for (int i = 0; i < MT; ++i)
+      for (int u = 0; u < NDX; ++u) {
+        const int row = 2 * u + (lane >> 5);
+        xsrc[u] = xrow_ptr(r0, row) + pb * 256 + 16 * ((lane & 31) ^ (row & 15));
+      }
+    } else {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) B.xa[i][j] = *reinterpret_cast<const g_u32x4_t*>(xr[i] + b * 256 + 64 * j);
+      for (int i = 0; i < MT; ++i) xr[i] = xrow_ptr(r0, 16 * i + r) + pb * 256 + 16 * q;
+    }
+    // the compiler's own loads (scales, indices) are complete before the
+    // counted loads of the K loop start
+    __builtin_amdgcn_s_waitcnt(0);
+    g_u32x4_t xreg[XL ? 1 : D][2][MT][4];
+    auto issue = [&](int st, int slot) {
 #pragma unroll
-      for (int tt = 0; tt < NT; ++tt)
-        B.wv[tt] = __builtin_nontemporal_load(reinterpret_cast<const g_u32x4_t*>(wr[tt] + b * 64));
+      for (int u = 0; u < NDW; ++u) dma16(wsrc[u] + st * 128, lds_wave + slot * SSTAGE + u * 1024);
+      if constexpr (XL) {
+#pragma unroll
+        for (int u = 0; u < NDX; ++u) dma16(xsrc[u] + st * 512, lds_wave + slot * SSTAGE + WSTAGE + u * 1024);
+      } else {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) xreg[slot][h][i][j] = gload16(xr[i] + (2 * st + h) * 256 + 64 * j);
+      }
     };
     f32x4d_t Y[NT][MT];
 #pragma unroll
     for (int tt = 0; tt < NT; ++tt)
 #pragma unroll
       for (int i = 0; i < MT; ++i) Y[tt][i] = f32x4d_t{0.f, 0.f, 0.f, 0.f};
-    auto compute = [&](const Blk& B, int b) {
+    auto compute = [&](int slot, int h, int b) {
       g_u32x4_t A[MT][4];
 #pragma unroll
       for (int i = 0; i < MT; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const g_u32x4_t v = B.xa[i][j];
-          A[i][j] = g_u32x4_t{__builtin_amdgcn_perm(v.z, v.x, 0x05040100u), __builtin_amdgcn_perm(v.z, v.x, 0x07060302u),
-                              __builtin_amdgcn_perm(v.w, v.y, 0x05040100u), __builtin_amdgcn_perm(v.w, v.y, 0x07060302u)};
-        }
-      f32x4d_t XG[MT][GB];
-#pragma unroll
-      for (int i = 0; i < MT; ++i)
-#pragma unroll
-        for (int g = 0; g < GB; ++g) {
-          XG[i][g] = mfma16<XT>(A[i][g * JG], ones, f32x4d_t{0.f, 0.f, 0.f, 0.f});
-#pragma unroll
-          for (int j = 1; j < JG; ++j) XG[i][g] = mfma16<XT>(A[i][g * JG + j], ones, XG[i][g]);
-        }
-#pragma unroll
-      for (int tt = 0; tt < NT; ++tt) {
-        uint32_t wd[4] = {B.wv[tt].x, B.wv[tt].y, B.wv[tt].z, B.wv[tt].w};
-        auto s02 = __builtin_amdgcn_permlane32_swap(wd[0], wd[2], false, false);
-        auto s13 = __builtin_amdgcn_permlane32_swap(wd[1], wd[3], false, false);
-        auto s01 = __builtin_amdgcn_permlane16_swap(s02[0], s13[0], false, false);
-        auto s23 = __builtin_amdgcn_permlane16_swap(s02[1], s13[1], false, false);
-        wd[0] = s01[0]; wd[1] = s01[1]; wd[2] = s23[0]; wd[3] = s23[1];
-        g_u32x4_t Wp[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint32_t lo = wd[j] & 0x0F0F0F0Fu, hi = (wd[j] >> 4) & 0x0F0F0F0Fu;
-          Wp[j] = g_u32x4_t{__builtin_amdgcn_perm(EB, lo, 0x04020400u), __builtin_amdgcn_perm(EB, hi, 0x04020400u),
-                            __builtin_amdgcn_perm(EB, lo, 0x04030401u), __builtin_amdgcn_perm(EB, hi, 0x04030401u)};
-        }
-#pragma unroll
-        for (int g = 0; g < GB; ++g) {
-          const int hf = b * GB + g;
-          const float s = to_f<XT>(static_cast<XS>(sw[tt][hf >> 1] >> (16 * (hf & 1))));
-          const float bs = to_f<XT>(static_cast<XS>(bw[tt][hf >> 1] >> (16 * (hf & 1))));
-          const float cb = fmaf(-CM, s, bs);
-#pragma unroll
-          for (int i = 0; i < MT; ++i) {
-            f32x4d_t Dd = mfma16<XT>(A[i][g * JG], Wp[g * JG], f32x4d_t{0.f, 0.f, 0.f, 0.f});
-#pragma unroll
-            for (int j = 1; j < JG; ++j) Dd = mfma16<XT>(A[i][g * JG + j], Wp[g * JG + j], Dd);
-#pragma unroll
-            for (int v = 0; v < 4; ++v) Y[tt][i][v] = fmaf(s, Dd[v], fmaf(cb, XG[i][g][v], Y[tt][i][v]));
+          if constexpr (XL) {
+            const int m = 16 * i + r, p = 16 * h + 4 * j + q;
+            A[i][j] = x_pairs(
+                *reinterpret_cast<const g_u32x4_t*>(lds_w + slot * SSTAGE + WSTAGE + m * 512 + 16 * (p ^ (m & 15))));
+          } else {
+            A[i][j] = x_pairs(xreg[slot][h][i][j]);
           }
         }
-      }
+      fac_block<XT, NT, MT, GB, SW>(Y, A, lds_w + slot * SSTAGE, h, b * GB, sw, bw, r, q);
     };
-    Blk ring[D];
 #pragma unroll
-    for (int d = 0; d < D && d < KB; ++d) load(d, ring[d]);
+    for (int st = 0; st < D && st < NS; ++st) issue(st, st);
 #pragma unroll
-    for (int b = 0; b < KB; ++b) {
-      compute(ring[b % D], b);
-      if (b + D < KB) load(b + D, ring[b % D]);
+    for (int st = 0; st < NS; ++st) {
+      const int slot = st % D;
+      const int later = st + D <= NS ? D - 1 : NS - 1 - st;
+      if (later == 2) vm_wait<(D >= 3 ? 2 * PER : 0)>();
+      else if (later == 1) vm_wait<PER>();
+      else vm_wait<0>();
+      if constexpr (!XL) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) asm volatile("" : "+v"(xreg[slot][h][i][j])::"memory");
+      }
+      compute(slot, 0, 2 * st);
+      compute(slot, 1, 2 * st + 1);
+      if (st + D < NS) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        issue(st + D, slot);
+      }
     }
-    // row rr = r0 + 16 i + 4 q + v of the expert, column n0 + 16 tt + r
-    auto store = [&](int64_t rr, int col, float g, float u) {
-      const int64_t b = blo + rr / Mx, mrow = rr % Mx;
-      const int64_t xm = a.bm.lhs ? load_index(a.bm.lhs, a.bm.lhs_dt, b) : b;
-      const bool ok = xm >= 0 && xm < a.bm.nx;
+    // row rr = r0 + m of the expert, column col
+    auto store = [&](int m, int col, float g, float u) {
+      const int64_t o = prow_o[m];
       const auto v = GLU ? swiglu_out<XT>(g, u) : from_f<XT>(g);
-      out[(b * Mx + mrow) * N + col] = ok ? v : from_f<XT>(__builtin_nanf(""));
+      if (o >= 0) out[o + col] = v;
+      else out[~o + col] = from_f<XT>(__builtin_nanf(""));
     };
     if constexpr (S == 1) {
 #pragma unroll
@@ -184,15 +227,18 @@ __global__ __launch_bounds__(64 * S) void gather_decode_kernel(QmmArgs a, int64_
           for (int v = 0; v < 4; ++v) {
             const int64_t rr = r0 + 16 * i + 4 * q + v;
             const int col = n0 + 16 * tt + r;
-            if (rr < rows_total && col < N) store(rr, col, Y[tt][i][v], GLU ? Y[tt + NT / 2][i][v] : 0.f);
+            if (rr < rows_total && col < N) store(16 * i + 4 * q + v, col, Y[tt][i][v], GLU ? Y[tt + NT / 2][i][v] : 0.f);
           }
+      __syncthreads();  // the ring and row tables are refilled by the next pass
     } else {
+      __syncthreads();  // every wave's ring reads are done before the partials overwrite LDS
+      float* red = reinterpret_cast<float*>(lds);
 #pragma unroll
       for (int tt = 0; tt < NT; ++tt)
 #pragma unroll
         for (int i = 0; i < MT; ++i)
 #pragma unroll
-          for (int v = 0; v < 4; ++v) red[((wave * NT + tt) * 2 + i) * 256 + (4 * q + v) * 16 + r] = Y[tt][i][v];
+          for (int v = 0; v < 4; ++v) red[((wave * NT + tt) * MT + i) * 256 + (4 * q + v) * 16 + r] = Y[tt][i][v];
       __syncthreads();
       for (int idx = t; idx < 16 * MT * NC; idx += 64 * S) {
         const int m = idx / NC, nn = idx % NC;
@@ -201,56 +247,82 @@ __global__ __launch_bounds__(64 * S) void gather_decode_kernel(QmmArgs a, int64_
         if (rr >= rows_total || n0 + nn >= N) continue;
         float acc[2] = {0.f, 0.f};
 #pragma unroll
-        for (int h = 0; h < (GLU ? 2 : 1); ++h) {
-          const int tt = GLU ? h * (NT / 2) + (nn >> 4) : (nn >> 4);
+        for (int hh = 0; hh < (GLU ? 2 : 1); ++hh) {
+          const int tt = GLU ? hh * (NT / 2) + (nn >> 4) : (nn >> 4);
 #pragma unroll
-          for (int w2 = 0; w2 < S; ++w2) acc[h] += red[((w2 * NT + tt) * 2 + i) * 256 + mr * 16 + (nn & 15)];
+          for (int w2 = 0; w2 < S; ++w2) acc[hh] += red[((w2 * NT + tt) * MT + i) * 256 + mr * 16 + (nn & 15)];
         }
-        store(rr, n0 + nn, acc[0], acc[1]);
+        store(m, n0 + nn, acc[0], acc[1]);
       }
-      __syncthreads();
+      __syncthreads();  // the partials are read before the next pass refills the ring
     }
   };
-  for (int64_t r0 = 0; r0 < rows_total; r0 += 32) {
-    if (rows_total - r0 > 16) pass(std::integral_constant<int, 2>{}, r0);
-    else pass(std::integral_constant<int, 1>{}, r0);
+  if constexpr (MTMAX == 2) {
+    for (int64_t r0 = 0; r0 < rows_total; r0 += 32) {
+      if (rows_total - r0 > 16) pass(std::integral_constant<int, 2>{}, r0);
+      else pass(std::integral_constant<int, 1>{}, r0);
+    }
+  } else {
+    for (int64_t r0 = 0; r0 < rows_total; r0 += 16) pass(std::integral_constant<int, 1>{}, r0);
   }
 }
 
 struct GatCfg {
   int nt, s, d, kb;
+  bool xl;
+  int mt;
 };
 
-// grouped configurations (measured, 256 experts, top 8, q4 gs 64): K = 2048
-// (gate / up) four waves of four blocks; K = 512 (down) two waves of two
+// Measured (256 experts, top 8, q4 gs 64, bf16, T = 64 / 512): four 16-row
+// tiles per workgroup, x in registers, passes of 16 rows (two-tile MT passes
+// need more registers than the extra weight re-reads cost: T = 512 gate
+// 83.6 -> 65.1 us); K = 2048 (gate) four waves of four blocks, K = 512
+// (down) two waves of two.  Other K: four waves when K / 128 is 8, 16 or 32,
+// two when 4 (longer K ranges would keep more scale words in registers than
+// fit next to the x ring; those shapes take the generic grouped kernel).
 GatCfg gather_choose(const QmmArgs& a) {
   const int P = a.K >> 7;
-  if (P % 4 == 0 && P / 4 <= 8) return GatCfg{4, 4, 2, P / 4};
-  if (P % 2 == 0 && P / 2 <= 8) return GatCfg{4, 2, 2, P / 2};
-  return GatCfg{0, 0, 0, 0};
+  GatCfg c{0, 0, 0, 0, false, 1};
+  if (P == 8 || P == 16 || P == 32) c = GatCfg{4, 4, 2, P / 4, false, 1};
+  else if (P == 4) c = GatCfg{4, 2, 2, 2, false, 1};
+  else if (P == 2) c = GatCfg{4, 1, 2, 2, false, 1};
+  return c;
+}
+
+template <int XT, int GB, bool GLU, int NT, int S, int D, int KB, bool XL, int MT>
+hipError_t gat_go(const QmmArgs& a, int64_t nflat, int64_t E, const int64_t* off) {
+  if constexpr ((GLU && NT % 2 != 0) || KB % 2 != 0 || !gat_fits<NT, MT, S, D, XL, KB>()) {
+    return hipErrorInvalidValue;
+  } else {
+    constexpr int NC = GLU ? 8 * NT : 16 * NT;
+    const dim3 grid(static_cast<unsigned>((a.N + NC - 1) / NC * (E + 1)));
+    hipLaunchKernelGGL((gather_decode_kernel<XT, NT, GB, S, D, KB, XL, GLU, MT>), grid, dim3(64 * S), 0, a.stream, a,
+                       nflat, off);
+    return hipGetLastError();
+  }
+}
+
+#define IQMM_GAT_CONFIGS(X)                                                                             \
+  X(4, 4, 2, 2, false, 1) X(4, 4, 2, 4, false, 1) X(4, 4, 2, 8, false, 1)                              \
+  X(4, 2, 2, 2, false, 1) X(4, 1, 2, 2, false, 1)
+
+bool gat_instantiated(const GatCfg& c) {
+  bool ok = false;
+#define IQMM_GAT_K(NT_, S_, D_, KB_, XL_, MT_) \
+  ok = ok || (c.nt == NT_ && c.s == S_ && c.d == D_ && c.kb == KB_ && c.xl == XL_ && c.mt == MT_ && gat_fits<NT_, MT_, S_, D_, XL_, KB_>());
+  IQMM_GAT_CONFIGS(IQMM_GAT_K)
+#undef IQMM_GAT_K
+  return ok;
 }
 
 template <int XT, int GB, bool GLU>
 hipError_t gather_dec_go(const QmmArgs& a, int64_t nflat, int64_t E, const int64_t* off) {
   const GatCfg c = gather_choose(a);
-  constexpr int NT = 4;
-  constexpr int NC = GLU ? 8 * NT : 16 * NT;
-  const dim3 grid(static_cast<unsigned>((a.N + NC - 1) / NC), static_cast<unsigned>(E + 1));
-#define IQMM_GDEC(S_, D_, KB_)                                                                                     \
-  if (c.s == S_ && c.d == D_ && c.kb == KB_) {                                                                     \
-    hipLaunchKernelGGL((gather_decode_kernel<XT, NT, GB, S_, D_, KB_, GLU>), grid, dim3(64 * S_), 0, a.stream, a, \
-                       nflat, off);                                                                                \
-    return hipGetLastError();                                                                                      \
-  }
-  IQMM_GDEC(4, 2, 4)
-  IQMM_GDEC(4, 2, 2)
-  IQMM_GDEC(4, 2, 8)
-  IQMM_GDEC(2, 2, 2)
-  IQMM_GDEC(2, 2, 4)
-  IQMM_GDEC(2, 2, 8)
-  IQMM_GDEC(4, 2, 1)
-  IQMM_GDEC(2, 2, 1)
-#undef IQMM_GDEC
+#define IQMM_GAT(NT_, S_, D_, KB_, XL_, MT_)                                                              \
+  if (c.nt == NT_ && c.s == S_ && c.d == D_ && c.kb == KB_ && c.xl == XL_ && c.mt == MT_)                \
+    return gat_go<XT, GB, GLU, NT_, S_, D_, KB_, XL_, MT_>(a, nflat, E, off);
+  IQMM_GAT_CONFIGS(IQMM_GAT)
+#undef IQMM_GAT
   return hipErrorInvalidValue;
 }
 
@@ -263,6 +335,7 @@ hipError_t gather_dec_gs(const QmmArgs& a, int64_t nflat, int64_t E, const int64
   }
 }
 
+
 }  // namespace
 
 bool gather_decode_supported(const QmmArgs& a) {
@@ -271,8 +344,7 @@ bool gather_decode_supported(const QmmArgs& a) {
     return false;
   if (a.gs != 32 && a.gs != 64 && a.gs != 128) return false;
   const GatCfg c = gather_choose(a);
-  if (c.kb == 0) return false;
-  if (a.gs == 128 && c.kb % 2 != 0) return false;
+  if (c.kb == 0 || c.s * c.kb * 128 != a.K || !gat_instantiated(c)) return false;
   return (reinterpret_cast<uintptr_t>(a.s) | reinterpret_cast<uintptr_t>(a.b)) % 4 == 0 && ((a.K / a.gs) * 2) % 4 == 0;
 }
 
