@@ -538,10 +538,10 @@ int gather_entry(const char* op, iqmm_array* res, iqmm_array x, iqmm_array w, iq
                           (present(lhs) ? numel(lhs) == a.nbatch : nxm == a.nbatch);
   // Sorted rows go to the grouped kernel (each expert's weights read once for
   // all of its rows), except where the M = 1 GEMV applies and experts hold at
-  // most 4 rows on average: there the per-row GEMV, whose repeated weight
-  // reads hit the caches, was measured as fast or faster (T = 64 of a
-  // 256-expert top-8 routing: gate projection 54.5 against 57.5 us, the
-  // fused-SwiGLU expert block equal).  The fused SwiGLU follows the same choice.
+  // most one row on average: there the per-row GEMV is as fast (T = 8 of a
+  // 256-expert top-8 routing: gate projection 11.9 against 12.6 us; at T = 64
+  // the grouped kernel takes 41.5 against 54.2 us).  The fused SwiGLU follows
+  // the same choice.
   const int64_t rows_per_expert = a.nbatch * a.M / (nwm > 0 ? nwm : 1);
   QmmArgs probe = a;
   probe.N = glu ? 2 * a.N : a.N;
@@ -551,7 +551,7 @@ int gather_entry(const char* op, iqmm_array* res, iqmm_array x, iqmm_array w, iq
   // block: 189 against 194 us).
   const bool glu_grouped = glu && a.nbatch * a.M >= 512 && gather_sorted_glu_supported(a);
   const bool grouped = sorted_indices && one_to_one && nwm + 1 <= 65535 && gather_sorted_supported(a) &&
-                       (glu_grouped || !(gemv_ok && rows_per_expert <= 4));
+                       (glu_grouped || !(gemv_ok && rows_per_expert <= 1));
   auto product = [&](QmmArgs& p) { return grouped ? launch_gather_sorted(p, p.nbatch, nwm) : run_qmm(p); };
   hipError_t e;
   if (glu && grouped && gather_sorted_glu_supported(a)) {
