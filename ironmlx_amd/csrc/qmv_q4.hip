@@ -169,7 +169,7 @@ struct Q4Args {
 // gate_up layout); a wave reduces RB / 2 gate rows and the matching up rows
 // and writes RB / 2 SwiGLU outputs.
 template <int XT, int RB, int CPL, bool MAPPED, int MR, int MODE = AFFINE, bool GLU = false>
-__global__ __launch_bounds__(64) void qmv_q4_kernel(Q4Args p, BatchMap bm, int64_t batch0) {
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(MR == 1 && RB == 2 && CPL == 2 ? 7 : 1))) void qmv_q4_kernel(Q4Args p, BatchMap bm, int64_t batch0) {
   static_assert(!GLU || (MR == 1 && RB % 2 == 0), "GLU pairs gate / up rows at M = 1");
   constexpr int RO = GLU ? RB / 2 : RB;  // outputs per wave
   using XS = uint16_t;
