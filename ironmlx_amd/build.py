@@ -29,20 +29,37 @@ FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
 
 # Kernels whose K loops load into registers with inline assembly and wait with
 # explicit vmcnt: the compiler treats such an output as written when the asm
-# statement issues, so a kernel that spills (or otherwise moves a register
-# before its load has landed) would read stale data or have a late load
-# overwrite a register reused meanwhile.  Their files are compiled with the
-# resource-usage report and the build fails if any kernel uses scratch.
+# statement issues, so a kernel that spills or copies a register before its
+# load has landed (to scratch, or to an AGPR when the 256 VGPRs are used up)
+# reads stale data, or has the late load overwrite a register reused
+# meanwhile.  Their files are compiled with the resource-usage report and the
+# build fails for any kernel that uses scratch, reaches the VGPR limit, or
+# (files built with MFMA results in VGPRs) uses AGPRs at all.
 NO_SCRATCH = {"qmm_decode.hip", "qmm_gather.hip"}
 
 
-def scratch_kernels(remarks: str) -> list[str]:
-    """Kernels of a -Rpass-analysis=kernel-resource-usage report with scratch."""
+def register_loads(name: str) -> bool:
+    """Whether a qmm_decode_kernel / gather_decode_kernel instantiation loads x
+    into registers: its first bool template argument (XL, x through LDS) is 0."""
+    m = re.search(r"_kernelI.*?Lb([01])E", name)
+    return not (m and m.group(1) == "1")
+
+
+def spilling_kernels(remarks: str, agprs_allowed: bool = True) -> list[str]:
+    """Kernels of a -Rpass-analysis=kernel-resource-usage report that load into
+    registers (register_loads) and use scratch, all 256 VGPRs, or
+    (agprs_allowed False) any AGPR."""
     out = []
     for block in remarks.split("remark: Function Name: ")[1:]:
         name = block.split()[0]
-        m = re.search(r"ScratchSize \[bytes/lane\]: (\d+)", block)
-        if m and int(m.group(1)) > 0:
+        if not register_loads(name):
+            continue
+
+        def field(key):
+            m = re.search(key + r": (\d+)", block)
+            return int(m.group(1)) if m else 0
+        if (field(r"ScratchSize \[bytes/lane\]") > 0 or field("VGPRs") >= 256
+                or (not agprs_allowed and field("AGPRs") > 0)):
             out.append(name)
     return out
 
@@ -55,7 +72,7 @@ def _compile(src: str) -> str:
     if p.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{p.stderr}")
     if src in NO_SCRATCH:
-        bad = scratch_kernels(p.stderr)
+        bad = spilling_kernels(p.stderr, agprs_allowed="-amdgpu-mfma-vgpr-form" not in FILE_FLAGS.get(src, []))
         if bad:
             os.remove(obj)
             raise RuntimeError(f"{src}: kernels with register loads in flight use scratch: {bad[:8]}")

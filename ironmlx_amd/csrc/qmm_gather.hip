@@ -277,21 +277,31 @@ struct GatCfg {
 // tiles per workgroup, x in registers, passes of 16 rows (two-tile MT passes
 // need more registers than the extra weight re-reads cost: T = 512 gate
 // 83.6 -> 65.1 us); K = 2048 (gate) four waves of four blocks, K = 512
-// (down) two waves of two.  Other K: four waves when K / 128 is 8, 16 or 32,
-// two when 4 (longer K ranges would keep more scale words in registers than
-// fit next to the x ring; those shapes take the generic grouped kernel).
+// (down) two waves of two.  A wave's K range is at most four blocks (two at
+// gs 32, whose scale words take twice the registers), so that the kernel
+// stays below the VGPR limit next to its x ring; other K take the generic
+// grouped kernel.
 GatCfg gather_choose(const QmmArgs& a) {
   const int P = a.K >> 7;
+  const int kb = a.gs == 32 ? 2 : 4;  // blocks per wave
   GatCfg c{0, 0, 0, 0, false, 1};
-  if (P == 8 || P == 16 || P == 32) c = GatCfg{4, 4, 2, P / 4, false, 1};
-  else if (P == 4) c = GatCfg{4, 2, 2, 2, false, 1};
-  else if (P == 2) c = GatCfg{4, 1, 2, 2, false, 1};
+  if (P == 4) c = GatCfg{4, 2, 2, 2, false, 1};
+  else if (P == 8) c = GatCfg{4, 4, 2, 2, false, 1};
+  else if (P == 16 || (P == 32 && kb == 4)) c = GatCfg{4, P / kb, 2, kb, false, 1};
+  else if (P == 2 && a.gs != 32) c = GatCfg{4, 1, 2, 2, false, 1};
   return c;
+}
+
+// instantiations whose register use reaches the VGPR limit (scale words of
+// long K ranges at gs 32) are never produced by gather_choose
+template <int GB, int S, int KB>
+constexpr bool gat_regs_ok() {
+  return !(GB == 4 && (KB >= 4 || S == 1));
 }
 
 template <int XT, int GB, bool GLU, int NT, int S, int D, int KB, bool XL, int MT>
 hipError_t gat_go(const QmmArgs& a, int64_t nflat, int64_t E, const int64_t* off) {
-  if constexpr ((GLU && NT % 2 != 0) || KB % 2 != 0 || !gat_fits<NT, MT, S, D, XL, KB>()) {
+  if constexpr ((GLU && NT % 2 != 0) || KB % 2 != 0 || !gat_fits<NT, MT, S, D, XL, KB>() || !gat_regs_ok<GB, S, KB>()) {
     return hipErrorInvalidValue;
   } else {
     constexpr int NC = GLU ? 8 * NT : 16 * NT;
@@ -303,13 +313,15 @@ hipError_t gat_go(const QmmArgs& a, int64_t nflat, int64_t E, const int64_t* off
 }
 
 #define IQMM_GAT_CONFIGS(X)                                                                             \
-  X(4, 4, 2, 2, false, 1) X(4, 4, 2, 4, false, 1) X(4, 4, 2, 8, false, 1)                              \
-  X(4, 2, 2, 2, false, 1) X(4, 1, 2, 2, false, 1)
+  X(4, 2, 2, 2, false, 1) X(4, 4, 2, 2, false, 1) X(4, 4, 2, 4, false, 1) X(4, 8, 2, 2, false, 1)      \
+  X(4, 8, 2, 4, false, 1) X(4, 1, 2, 2, false, 1)
 
-bool gat_instantiated(const GatCfg& c) {
+bool gat_instantiated(const GatCfg& c, int gs) {
   bool ok = false;
-#define IQMM_GAT_K(NT_, S_, D_, KB_, XL_, MT_) \
-  ok = ok || (c.nt == NT_ && c.s == S_ && c.d == D_ && c.kb == KB_ && c.xl == XL_ && c.mt == MT_ && gat_fits<NT_, MT_, S_, D_, XL_, KB_>());
+#define IQMM_GAT_K(NT_, S_, D_, KB_, XL_, MT_)                                                                 \
+  ok = ok || (c.nt == NT_ && c.s == S_ && c.d == D_ && c.kb == KB_ && c.xl == XL_ && c.mt == MT_ &&              \
+              gat_fits<NT_, MT_, S_, D_, XL_, KB_>() &&                                                        \
+              (gs == 32 ? gat_regs_ok<4, S_, KB_>() : gs == 64 ? gat_regs_ok<2, S_, KB_>() : gat_regs_ok<1, S_, KB_>()));
   IQMM_GAT_CONFIGS(IQMM_GAT_K)
 #undef IQMM_GAT_K
   return ok;
@@ -344,7 +356,7 @@ bool gather_decode_supported(const QmmArgs& a) {
     return false;
   if (a.gs != 32 && a.gs != 64 && a.gs != 128) return false;
   const GatCfg c = gather_choose(a);
-  if (c.kb == 0 || c.s * c.kb * 128 != a.K || !gat_instantiated(c)) return false;
+  if (c.kb == 0 || c.s * c.kb * 128 != a.K || !gat_instantiated(c, a.gs)) return false;
   return (reinterpret_cast<uintptr_t>(a.s) | reinterpret_cast<uintptr_t>(a.b)) % 4 == 0 && ((a.K / a.gs) * 2) % 4 == 0;
 }
 
