@@ -475,6 +475,10 @@ def bench_fused(ops, Ms=(1, 4, 16), layers=32):
         td = _graph_layers([on_device], reps=10)
         tt = _graph_layers([torch_routing], reps=10)
         moe[str(T)] = {"device_routing_fused_us": round(td * 1e6, 2), "torch_routing_split_us": round(tt * 1e6, 2)}
+        if T == 1:
+            # route + experts + combine of one token in two launches (ops.moe_token)
+            tk = _graph_layers([lambda: dev.token_forward(x, logits)], reps=10)
+            moe[str(T)]["one_token_kernels_us"] = round(tk * 1e6, 2)
     out["qwen_moe_expert_block"] = moe
     del gu_w, down_w, fused_ex, split_ex
     torch.cuda.empty_cache()

@@ -260,6 +260,31 @@ int iqmm_moe_sort_noalloc(iqmm_array* res_tokens, iqmm_array* res_sorted, iqmm_a
 int iqmm_moe_combine(iqmm_array* res, iqmm_array y, iqmm_array inverse, iqmm_array experts,
                      iqmm_array scores, int num_experts, iqmm_stream stream);
 
+/*
+ * One token's routed experts in two launches: the routing of
+ * iqmm_moe_route, the fused gate_up SwiGLU of each routed expert
+ * (iqmm_gather_qmm_swiglu over the token's k rows) and the down projections
+ * with the ordered weighted combine of iqmm_moe_combine.  Replaces, for a
+ * single decode token, the per-expert loop of mlx/src/nn/moe.rs:55-183
+ * (route :67-82, experts :92-143, combine :146-168); mlx-c has no fused
+ * counterpart, so a binding calls it where the block would otherwise run
+ * route + gather + gather + combine for T = 1.
+ *   logits           [1, E] (or [E]) float32 | float16 | bfloat16
+ *   x                [1, H] bfloat16 | float16
+ *   gate_up_*        [E, 2I, H/8] uint32, scales / biases [E, 2I, H/gs] in x's
+ *                    dtype (gate rows first, as stacked by the checkpoint)
+ *   down_*           [E, D, I/8] uint32, scales / biases [E, D, I/gs]
+ *   res              [1, D] float32
+ * Affine 4-bit only; E <= 512, 1 <= k <= min(E, 32), H in [32, 8192] and
+ * I in [32, 2048] multiples of 32 and of the group size (32, 64 or 128).
+ * Uses a per-stream workspace of k * I * 2 + 256 bytes (sized beforehand for
+ * graph capture, as the other calls' workspaces).
+ */
+int iqmm_moe_token(iqmm_array* res, iqmm_array logits, iqmm_array x, iqmm_array gate_up_w,
+                   iqmm_array gate_up_scales, iqmm_array gate_up_biases, iqmm_array down_w,
+                   iqmm_array down_scales, iqmm_array down_biases, int k, bool norm_topk_prob,
+                   int group_size, int bits, iqmm_stream stream);
+
 /* Message of the last failed call on this thread ("" if none). */
 const char* iqmm_last_error(void);
 

@@ -33,7 +33,7 @@ class OptionalDtype(ctypes.Structure):
 EXPORTS = ("iqmm_quantized_matmul", "iqmm_dequantize", "iqmm_gather_qmm", "iqmm_quantize",
            "iqmm_quantized_swiglu", "iqmm_gather_qmm_swiglu", "iqmm_dequantize_rows",
            "iqmm_moe_route", "iqmm_moe_sort", "iqmm_moe_sort_noalloc", "iqmm_moe_combine",
-           "iqmm_workspace_reserve", "iqmm_last_error", "iqmm_version")
+           "iqmm_moe_token", "iqmm_workspace_reserve", "iqmm_last_error", "iqmm_version")
 
 _lib = None
 
@@ -77,6 +77,8 @@ def load() -> ctypes.CDLL:
     L.iqmm_moe_sort_noalloc.restype = ctypes.c_int
     L.iqmm_moe_combine.argtypes = [P, A, A, A, A, i, vp]
     L.iqmm_moe_combine.restype = ctypes.c_int
+    L.iqmm_moe_token.argtypes = [P, A, A, A, A, A, A, A, A, i, b, i, i, vp]
+    L.iqmm_moe_token.restype = ctypes.c_int
     L.iqmm_workspace_reserve.argtypes = [vp, ctypes.c_size_t]
     L.iqmm_workspace_reserve.restype = ctypes.c_int
     L.iqmm_last_error.restype = ctypes.c_char_p

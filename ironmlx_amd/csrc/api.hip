@@ -760,4 +760,56 @@ int iqmm_moe_combine(iqmm_array* res, iqmm_array y, iqmm_array inverse, iqmm_arr
   return e == hipSuccess ? 0 : hip_fail(op, e);
 }
 
+
+int iqmm_moe_token(iqmm_array* res, iqmm_array logits, iqmm_array x, iqmm_array gate_up_w,
+                   iqmm_array gate_up_scales, iqmm_array gate_up_biases, iqmm_array down_w,
+                   iqmm_array down_scales, iqmm_array down_biases, int k, bool norm_topk_prob,
+                   int group_size, int bits, iqmm_stream stream) {
+  const char* op = "moe_token";
+  g_last_error.clear();
+  if (!present(logits) || !is_float(logits.dtype)) return fail("[%s] logits must be a floating array [1, experts].", op);
+  const int64_t E = numel(logits);
+  if (logits.ndim < 1 || logits.shape[logits.ndim - 1] != E)
+    return fail("[%s] logits must hold one token's [experts] row, got %s.", op, shape_str(logits).c_str());
+  if (!present(x) || (x.dtype != IQMM_BFLOAT16 && x.dtype != IQMM_FLOAT16))
+    return fail("[%s] x must be bfloat16 or float16.", op);
+  const int64_t H = numel(x);
+  if (x.ndim < 1 || x.shape[x.ndim - 1] != H) return fail("[%s] x must hold one token's row, got %s.", op, shape_str(x).c_str());
+  if (bits != 4) return fail("[%s] only 4-bit affine experts are supported, got bits=%d.", op, bits);
+  auto check3 = [&](const iqmm_array& a, int dt, int64_t d0, int64_t d1, int64_t d2, const char* what) {
+    if (!present(a) || a.ndim != 3 || a.dtype != dt || a.shape[0] != d0 || a.shape[1] != d1 || a.shape[2] != d2)
+      return fail("[%s] %s must be %s [%lld, %lld, %lld], got %s %s.", op, what, dt_name(dt), (long long)d0,
+                  (long long)d1, (long long)d2, dt_name(a.dtype), shape_str(a).c_str());
+    return 0;
+  };
+  if (!present(gate_up_w) || gate_up_w.ndim != 3) return fail("[%s] gate_up weight must be 3D [experts, 2I, H/8].", op);
+  if (!present(down_w) || down_w.ndim != 3) return fail("[%s] down weight must be 3D [experts, D, I/8].", op);
+  const int64_t I2 = gate_up_w.shape[1], D = down_w.shape[1], I = I2 / 2;
+  if (I2 % 2 != 0) return fail("[%s] gate_up must stack 2I rows (gate rows first), got %lld.", op, (long long)I2);
+  if (group_size != 32 && group_size != 64 && group_size != 128)
+    return fail("[%s] group_size must be 32, 64 or 128, got %d.", op, group_size);
+  if (H % group_size != 0 || I % group_size != 0) return fail("[%s] H and I must be multiples of the group size.", op);
+  if (check3(gate_up_w, IQMM_UINT32, E, I2, H / 8, "gate_up weight") ||
+      check3(gate_up_scales, x.dtype, E, I2, H / group_size, "gate_up scales") ||
+      check3(gate_up_biases, x.dtype, E, I2, H / group_size, "gate_up biases") ||
+      check3(down_w, IQMM_UINT32, E, D, I / 8, "down weight") ||
+      check3(down_scales, x.dtype, E, D, I / group_size, "down scales") ||
+      check3(down_biases, x.dtype, E, D, I / group_size, "down biases"))
+    return 1;
+  if (E > 0x7fffffffLL || H > 0x7fffffffLL || I > 0x7fffffffLL || D > 0x7fffffffLL ||
+      !moe_token_supported(static_cast<int>(E), k, static_cast<int>(H), static_cast<int>(I), static_cast<int>(D), group_size))
+    return fail("[%s] unsupported shape: experts <= 512, 1 <= k <= min(experts, 32), H in [32, 8192] and I in "
+                "[32, 2048] multiples of 32 (got E=%lld k=%d H=%lld I=%lld).", op, (long long)E, k, (long long)H, (long long)I);
+  const std::vector<int64_t> shp = {1, D};
+  bool q;
+  if (set_or_check_res(op, res, shp, IQMM_FLOAT32, &q)) return 1;
+  if (q) return 0;
+  hipError_t e = launch_moe_token(logits.data, logits.dtype, x.data, x.dtype, static_cast<const uint32_t*>(gate_up_w.data),
+                                  gate_up_scales.data, gate_up_biases.data, static_cast<const uint32_t*>(down_w.data),
+                                  down_scales.data, down_biases.data, static_cast<int>(E), k, norm_topk_prob,
+                                  static_cast<int>(H), static_cast<int>(I), static_cast<int>(D), group_size,
+                                  static_cast<float*>(res->data), static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? 0 : hip_fail(op, e);
+}
+
 }  // extern "C"

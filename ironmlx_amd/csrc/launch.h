@@ -88,13 +88,19 @@ hipError_t launch_moe_sort(const int32_t* experts, int n, int k, int E, int32_t*
 // the same sort with its bucket counts in a fixed per-device array (allocates nothing)
 hipError_t launch_moe_sort_noalloc(const int32_t* experts, int n, int k, int E, int32_t* tokens, int32_t* sorted,
                                    int32_t* inverse, int32_t* offsets, hipStream_t st);
+// one token's MoE experts (route + fused gate_up SwiGLU + down + combine),
+// affine 4-bit (moe.hip)
+bool moe_token_supported(int E, int k, int H, int I, int D, int gs);
+hipError_t launch_moe_token(const void* logits, int lt, const void* x, int xt, const uint32_t* gw, const void* gsc,
+                            const void* gbi, const uint32_t* dw, const void* dsc, const void* dbi, int E, int k,
+                            bool norm, int H, int I, int D, int gs, float* out, hipStream_t st);
 hipError_t launch_moe_combine(const void* y, int dt, const int32_t* inverse, const int32_t* experts,
                               const float* scores, float* out, int T, int k, int64_t D, int E, int64_t n,
                               hipStream_t st);
 // Scratch of one call: the (device, stream, slot) buffer, grown outside
 // capture; during capture a request larger than the buffer fails with
 // hipErrorStreamCaptureUnsupported (nothing is allocated inside a graph).
-enum WsSlot : int { WS_SPLITK = 0, WS_GLU = 1, WS_OFFSETS = 2, WS_SORT = 3, WS_CONV = 4, WS_NSLOTS = 5 };
+enum WsSlot : int { WS_SPLITK = 0, WS_GLU = 1, WS_OFFSETS = 2, WS_SORT = 3, WS_CONV = 4, WS_MOE = 5, WS_NSLOTS = 6 };
 hipError_t workspace_get(hipStream_t st, int slot, size_t bytes, void** p);
 // grow every slot of the stream to at least `bytes` (outside capture)
 hipError_t workspace_reserve(hipStream_t st, size_t bytes);

@@ -16,6 +16,7 @@
 #include <mutex>
 
 #include "launch.h"
+#include "gemv_common.h"
 
 namespace iqmm {
 
@@ -71,19 +72,29 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+__device__ __forceinline__ uint32_t wave_umax(uint32_t v) {
+  v = max(v, wave_partner<0>(v));
+  v = max(v, wave_partner<1>(v));
+  v = max(v, wave_partner<2>(v));
+  v = max(v, wave_partner<3>(v));
+  v = max(v, wave_partner<4>(v));
+  v = max(v, wave_partner<5>(v));
+  return v;
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
   for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
   return v;
 }
 
-// PL = probabilities per lane (E <= 64 * PL)
+// One token's routing by one wave (PL probabilities per lane, E <= 64 PL):
+// lane i < k receives slot i's score (as stored: rounded to the logits' dtype,
+// normalised when `norm`) and expert, or NaN / -1 when no candidate is left
+// (NaN logits).
 template <int DT, int PL>
-__global__ __launch_bounds__(256) void moe_route_kernel(const typename Store<DT>::T* logits, float* scores,
-                                                        int32_t* experts, int T, int E, int k, int norm) {
+__device__ __forceinline__ void route_token(const typename Store<DT>::T* row, int E, int k, int norm, float& score,
+                                            int& expert) {
   const int lane = threadIdx.x & 63;
-  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (t >= T) return;  // wave-uniform
-  const typename Store<DT>::T* row = logits + static_cast<int64_t>(t) * E;
   float p[PL];
   float m = -__builtin_inff();
 #pragma unroll
@@ -110,33 +121,71 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const typename Store<DT>
   float mine = 0.f;  // lane i keeps slot i's probability / expert
   int myexp = 0;
   float tot = 0.f;
-  for (int i = 0; i < k; ++i) {
-    // lane-local best: largest p, then lowest expert id
-    float bv = -1.f;
-    int bi = 0x7fffffff;
+  if constexpr (DT != F32) {
+    // 16-bit probabilities: one 32-bit key per candidate, (p bits) << 16 |
+    // (0xFFFF - e), orders by p (non-negative: its bits order as unsigned),
+    // then by the lower expert id; 0 marks padding, NaN and taken entries, so
+    // each slot is one unsigned max over the wave
+    uint32_t key[PL];
 #pragma unroll
     for (int j = 0; j < PL; ++j) {
       const int e = lane + 64 * j;
-      if (p[j] > bv) { bv = p[j]; bi = e; }  // ascending e within a lane: ties keep the first
+      key[j] = p[j] >= 0.f ? (static_cast<uint32_t>(from_f<DT>(p[j])) << 16) | static_cast<uint32_t>(0xFFFF - e) : 0u;
     }
-    wave_argmax(bv, bi);
-    if ((bi & 63) == lane) {
+    for (int i = 0; i < k; ++i) {
+      uint32_t best = key[0];
 #pragma unroll
-      for (int j = 0; j < PL; ++j)
-        if (lane + 64 * j == bi) p[j] = -1.f;
+      for (int j = 1; j < PL; ++j) best = best > key[j] ? best : key[j];
+      best = wave_umax(best);
+#pragma unroll
+      for (int j = 0; j < PL; ++j) key[j] = key[j] == best ? 0u : key[j];
+      const float bv = best ? to_f<DT>(static_cast<typename Store<DT>::T>(best >> 16)) : -1.f;
+      const int bi = best ? 0xFFFF - static_cast<int>(best & 0xFFFFu) : 0x7fffffff;
+      if (lane == i) { mine = bv; myexp = bi; }
+      tot += bv;  // slot order, fp32
     }
-    if (lane == i) { mine = bv; myexp = bi; }
-    tot += bv;  // slot order, fp32
+  } else {
+    for (int i = 0; i < k; ++i) {
+      // lane-local best: largest p, then lowest expert id
+      float bv = -1.f;
+      int bi = 0x7fffffff;
+#pragma unroll
+      for (int j = 0; j < PL; ++j) {
+        const int e = lane + 64 * j;
+        if (p[j] > bv) { bv = p[j]; bi = e; }  // ascending e within a lane: ties keep the first
+      }
+      wave_argmax(bv, bi);
+      if ((bi & 63) == lane) {
+#pragma unroll
+        for (int j = 0; j < PL; ++j)
+          if (lane + 64 * j == bi) p[j] = -1.f;
+      }
+      if (lane == i) { mine = bv; myexp = bi; }
+      tot += bv;  // slot order, fp32
+    }
   }
+  float v = mine;
+  if (norm) {
+    const float den = to_f<DT>(from_f<DT>(tot));
+    v = to_f<DT>(from_f<DT>(mine / den));
+  }
+  // no candidate left (NaN logits): an invalid expert that combine skips
+  score = mine >= 0.f ? v : __builtin_nanf("");
+  expert = mine >= 0.f ? myexp : -1;
+}
+
+template <int DT, int PL>
+__global__ __launch_bounds__(256) void moe_route_kernel(const typename Store<DT>::T* logits, float* scores,
+                                                        int32_t* experts, int T, int E, int k, int norm) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;  // wave-uniform
+  float sc;
+  int ex;
+  route_token<DT, PL>(logits + static_cast<int64_t>(t) * E, E, k, norm, sc, ex);
   if (lane < k) {
-    float v = mine;
-    if (norm) {
-      const float den = to_f<DT>(from_f<DT>(tot));
-      v = to_f<DT>(from_f<DT>(mine / den));
-    }
-    // no candidate left (NaN logits): an invalid expert that combine skips
-    scores[static_cast<int64_t>(t) * k + lane] = mine >= 0.f ? v : __builtin_nanf("");
-    experts[static_cast<int64_t>(t) * k + lane] = mine >= 0.f ? myexp : -1;
+    scores[static_cast<int64_t>(t) * k + lane] = sc;
+    experts[static_cast<int64_t>(t) * k + lane] = ex;
   }
 }
 
@@ -351,6 +400,229 @@ hipError_t route_pl(const void* logits, float* scores, int32_t* experts, int T, 
   return hipGetLastError();
 }
 
+
+// ---------------------------------------------------------------------------
+// One token's MoE experts (T = 1 decode, mlx/src/nn/moe.rs:55-183 for a single
+// row): routing, the fused gate_up SwiGLU of the k routed experts and their
+// down projections with the ordered weighted combine, in two launches instead
+// of route + gather + gather + combine.  Affine 4-bit experts, x in the
+// scales' 16-bit type.
+struct TokArgs {
+  const void* logits;  // [E], dtype LT
+  const char* x;       // [H]
+  const uint32_t* gw;  // gate_up codes [E, 2I, H / 8]
+  const uint16_t* gs;  // gate_up scales / biases [E, 2I, H / gs]
+  const uint16_t* gb;
+  const uint32_t* dw;  // down codes [E, D, I / 8]
+  const uint16_t* ds;  // down scales / biases [E, D, I / gs]
+  const uint16_t* db;
+  uint16_t* h;         // [k, I] SwiGLU rows (workspace)
+  float* scores;       // [k] (workspace)
+  int32_t* experts;    // [k] (workspace)
+  float* out;          // [D]
+  int E, k, norm, H, I, D, gshift;
+};
+
+// Kernel 1: grid (ceil(I / 2), k), one wave each.  Every wave routes the
+// token (ALU work on 64 lanes instead of a launch of its own), takes slot
+// blockIdx.y's expert and reduces its gate rows o0, o0 + 1 and up rows
+// I + o0, I + o0 + 1 as the M = 1 GEMV does (lane l owns chunks l, l + 64,
+// ...), writing h[slot, o] = silu(gate) * up.
+template <int LT, int PL, int XT, int CPL>
+__global__ __launch_bounds__(64) void moe_token_glu_kernel(TokArgs a) {
+  using XS = uint16_t;
+  const int lane = threadIdx.x;
+  const int slot = blockIdx.y;
+  float sc;
+  int ex;
+  route_token<LT, PL>(static_cast<const typename Store<LT>::T*>(a.logits), a.E, a.k, a.norm, sc, ex);
+  const int e = __shfl(ex, slot, 64);
+  if (blockIdx.x == 0 && slot == 0 && lane < a.k) {
+    a.scores[lane] = sc;
+    a.experts[lane] = ex;
+  }
+  const int I = a.I, H = a.H, C = H >> 5;
+  const int o0 = blockIdx.x * 2;
+  XS* h = a.h + static_cast<int64_t>(slot) * I;
+  if (e < 0) return;  // the combine skips the slot
+  const int64_t wrow = H >> 1, srow = H >> a.gshift;
+  uint32_t P[CPL][16];
+  float xs[CPL];
+  int cidx[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    cidx[j] = min(lane + 64 * j, C - 1);
+    const u32x4_t* xc = reinterpret_cast<const u32x4_t*>(a.x + static_cast<int64_t>(cidx[j]) * 64);
+    uint32_t X[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const u32x4_t v = xc[i];
+      X[4 * i] = v.x; X[4 * i + 1] = v.y; X[4 * i + 2] = v.z; X[4 * i + 3] = v.w;
+    }
+    make_pairs<XT>(X, P[j], xs[j]);
+    if (lane + 64 * j >= C) xs[j] = 0.f;
+  }
+  float red[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int o = min(o0 + (r & 1), I - 1);
+    const int64_t row = static_cast<int64_t>(e) * 2 * I + (r < 2 ? o : I + o);
+    const char* wr = reinterpret_cast<const char*>(a.gw) + row * wrow;
+    float acc = 0.f;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const u32x4_t wv = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(wr + cidx[j] * 16));
+      const int64_t g = row * srow + ((cidx[j] << 5) >> a.gshift);
+      const float s = to_f<XT>(a.gs[g]), b = to_f<XT>(a.gb[g]);
+      float d = chunk_dot<XT>(wv, P[j]);
+      if (lane + 64 * j >= C) d = 0.f;
+      acc = fmaf(s, fmaf(-Magic<XT>::c, xs[j], d), fmaf(b, xs[j], acc));
+    }
+    red[r] = dpp_sum_to_lane63(acc);
+  }
+  if (lane == 63) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      if (o0 + i < I) h[o0 + i] = swiglu_out<XT>(red[i], red[2 + i]);
+  }
+}
+
+// 16-lane sum (a row of the wave), left in every lane of the row
+__device__ __forceinline__ float row16_sum(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));
+  return v;
+}
+
+// Kernel 2: grid ceil(D / TOK_RB), TOK_RB output columns per workgroup of
+// ceil(k / 4) waves.  The valid slots are ranked by (expert, slot) -- the
+// combine's order for rows in (token, slot) order -- and each 16-lane row of
+// wave w reduces the down row of the slot of rank 4 w + row (chunks c,
+// c + 16, ... of I / 32), so every slot's loads are in flight at once.  Each
+// product is rounded to the 16-bit type (the down gather's output), then the
+// column's ordered sum of score * y runs in fp32 as moe_combine_kernel's does.
+constexpr int TOK_RB = 4;
+template <int XT, int CPLD>
+__global__ __launch_bounds__(512) void moe_token_down_kernel(TokArgs a) {
+  __shared__ int order[32];
+  __shared__ float wt[32];
+  __shared__ float ys[TOK_RB][32];
+  __shared__ int nv_s;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int k = a.k, E = a.E, I = a.I, D = a.D, CI = I >> 5;
+  const int n0 = blockIdx.x * TOK_RB;
+  if (wave == 0) {
+    bool ok = false;
+    if (lane < k) {
+      const int ex = a.experts[lane];
+      ok = ex >= 0 && ex < E;
+      int rank = 0;
+      for (int j = 0; j < k; ++j) {
+        const int ej = a.experts[j];
+        const bool okj = ej >= 0 && ej < E;
+        rank += (okj && (ej < ex || (ej == ex && j < lane))) ? 1 : 0;
+      }
+      if (ok) {
+        order[rank] = lane;
+        wt[rank] = a.scores[lane];
+      }
+    }
+    const int nv = __popcll(__ballot(ok));
+    if (lane == 0) nv_s = nv;
+  }
+  __syncthreads();
+  const int nv = nv_s;
+  const int g = lane >> 4, c = lane & 15;
+  const int64_t wrow = I >> 1, srow = I >> a.gshift;
+  if (4 * wave < nv) {  // wave-uniform
+    const int r = min(4 * wave + g, nv - 1);
+    const int slot = order[r];
+    const int e = a.experts[slot];
+    const char* hb = reinterpret_cast<const char*>(a.h + static_cast<int64_t>(slot) * I);
+    uint32_t P[CPLD][16];
+    float xs[CPLD];
+    int cidx[CPLD];
+#pragma unroll
+    for (int j = 0; j < CPLD; ++j) {
+      cidx[j] = min(c + 16 * j, CI - 1);
+      const u32x4_t* xc = reinterpret_cast<const u32x4_t*>(hb + static_cast<int64_t>(cidx[j]) * 64);
+      uint32_t X[16];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const u32x4_t v = xc[i];
+        X[4 * i] = v.x; X[4 * i + 1] = v.y; X[4 * i + 2] = v.z; X[4 * i + 3] = v.w;
+      }
+      make_pairs<XT>(X, P[j], xs[j]);
+      if (c + 16 * j >= CI) xs[j] = 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < TOK_RB; ++i) {
+      const int64_t row = static_cast<int64_t>(e) * D + min(n0 + i, D - 1);
+      const char* wr = reinterpret_cast<const char*>(a.dw) + row * wrow;
+      float acc = 0.f;
+#pragma unroll
+      for (int j = 0; j < CPLD; ++j) {
+        const u32x4_t wv = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(wr + cidx[j] * 16));
+        const int64_t gi = row * srow + ((cidx[j] << 5) >> a.gshift);
+        const float s = to_f<XT>(a.ds[gi]), b = to_f<XT>(a.db[gi]);
+        float d = chunk_dot<XT>(wv, P[j]);
+        if (c + 16 * j >= CI) d = 0.f;
+        acc = fmaf(s, fmaf(-Magic<XT>::c, xs[j], d), fmaf(b, xs[j], acc));
+      }
+      acc = row16_sum(acc);
+      if (c == 0 && 4 * wave + g < nv) ys[i][4 * wave + g] = to_f<XT>(from_f<XT>(acc));
+    }
+  }
+  __syncthreads();
+  if (t < TOK_RB && n0 + t < D) {
+    float acc = 0.f;
+    for (int r = 0; r < nv; ++r) {
+      const float p = ys[t][r] * wt[r];
+      acc = r == 0 ? p : acc + p;
+    }
+    a.out[n0 + t] = acc;
+  }
+}
+
+template <int LT, int PL, int XT>
+hipError_t token_glu_cpl(const TokArgs& a, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>((a.I + 1) / 2), static_cast<unsigned>(a.k));
+  switch (((a.H >> 5) + 63) / 64) {
+    case 1: hipLaunchKernelGGL((moe_token_glu_kernel<LT, PL, XT, 1>), grid, dim3(64), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((moe_token_glu_kernel<LT, PL, XT, 2>), grid, dim3(64), 0, st, a); break;
+    case 3: hipLaunchKernelGGL((moe_token_glu_kernel<LT, PL, XT, 3>), grid, dim3(64), 0, st, a); break;
+    default: hipLaunchKernelGGL((moe_token_glu_kernel<LT, PL, XT, 4>), grid, dim3(64), 0, st, a); break;
+  }
+  return hipGetLastError();
+}
+
+template <int LT, int XT>
+hipError_t token_glu_pl(const TokArgs& a, hipStream_t st) {
+  const int pl = (a.E + 63) / 64;
+  if (pl <= 1) return token_glu_cpl<LT, 1, XT>(a, st);
+  if (pl <= 2) return token_glu_cpl<LT, 2, XT>(a, st);
+  if (pl <= 4) return token_glu_cpl<LT, 4, XT>(a, st);
+  return token_glu_cpl<LT, 8, XT>(a, st);
+}
+
+template <int XT>
+hipError_t token_run(const TokArgs& a, int lt, hipStream_t st) {
+  hipError_t e = lt == F32 ? token_glu_pl<F32, XT>(a, st)
+                           : lt == F16 ? token_glu_pl<F16, XT>(a, st) : token_glu_pl<BF16, XT>(a, st);
+  if (e != hipSuccess) return e;
+  const dim3 grid(static_cast<unsigned>((a.D + TOK_RB - 1) / TOK_RB));
+  const dim3 block(64 * ((a.k + 3) / 4));
+  switch (((a.I >> 5) + 15) / 16) {
+    case 1: hipLaunchKernelGGL((moe_token_down_kernel<XT, 1>), grid, block, 0, st, a); break;
+    case 2: hipLaunchKernelGGL((moe_token_down_kernel<XT, 2>), grid, block, 0, st, a); break;
+    case 3: hipLaunchKernelGGL((moe_token_down_kernel<XT, 3>), grid, block, 0, st, a); break;
+    default: hipLaunchKernelGGL((moe_token_down_kernel<XT, 4>), grid, block, 0, st, a); break;
+  }
+  return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t launch_moe_route(const void* logits, int dt, float* scores, int32_t* experts, int T, int E, int k,
@@ -480,6 +752,44 @@ hipError_t launch_moe_combine(const void* y, int dt, const int32_t* inverse, con
       return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+
+bool moe_token_supported(int E, int k, int H, int I, int D, int gs) {
+  return E >= 1 && E <= 512 && k >= 1 && k <= 32 && k <= E && H % 32 == 0 && H >= 32 && H <= 8192 && I % 32 == 0 &&
+         I >= 32 && I <= 2048 && D >= 1 && (gs == 32 || gs == 64 || gs == 128);
+}
+
+hipError_t launch_moe_token(const void* logits, int lt, const void* x, int xt, const uint32_t* gw, const void* gsc,
+                            const void* gbi, const uint32_t* dw, const void* dsc, const void* dbi, int E, int k,
+                            bool norm, int H, int I, int D, int gs, float* out, hipStream_t st) {
+  if (!moe_token_supported(E, k, H, I, D, gs) || (xt != BF16 && xt != F16)) return hipErrorInvalidValue;
+  // workspace: h [k, I] (16-bit), then scores [k] and experts [k] (128 B each)
+  const size_t hbytes = (static_cast<size_t>(k) * I * 2 + 255) / 256 * 256;
+  void* ws = nullptr;
+  hipError_t e = workspace_get(st, WS_MOE, hbytes + 2 * 128, &ws);
+  if (e != hipSuccess) return e;
+  TokArgs a;
+  a.logits = logits;
+  a.x = static_cast<const char*>(x);
+  a.gw = gw;
+  a.gs = static_cast<const uint16_t*>(gsc);
+  a.gb = static_cast<const uint16_t*>(gbi);
+  a.dw = dw;
+  a.ds = static_cast<const uint16_t*>(dsc);
+  a.db = static_cast<const uint16_t*>(dbi);
+  a.h = static_cast<uint16_t*>(ws);
+  a.scores = reinterpret_cast<float*>(static_cast<char*>(ws) + hbytes);
+  a.experts = reinterpret_cast<int32_t*>(static_cast<char*>(ws) + hbytes + 128);
+  a.out = out;
+  a.E = E;
+  a.k = k;
+  a.norm = norm ? 1 : 0;
+  a.H = H;
+  a.I = I;
+  a.D = D;
+  a.gshift = __builtin_ctz(gs);
+  return xt == BF16 ? token_run<BF16>(a, lt, st) : token_run<F16>(a, lt, st);
 }
 
 }  // namespace iqmm

@@ -310,11 +310,33 @@ class MoEMLP:
         y = _gqmm(h, self.experts["down"], rhs, sorted_indices=srt, stream=stream)
         return ops.moe_combine(y, inverse, idx, scores.contiguous(), E, stream)
 
+    def _token_path(self, x_flat) -> bool:
+        """One decode token with fused affine 4-bit gate_up experts: route,
+        experts and combine run as :func:`ops.moe_token` (two launches)."""
+        gu, dn = self.experts.get("gate_up"), self.experts["down"]
+        if x_flat.shape[0] != 1 or gu is None:
+            return False
+        return all(e.mode == "affine" and e.bits == 4 and e.group_size in (32, 64, 128) and
+                   e.biases is not None and e.scales.dtype == x_flat.dtype for e in (gu, dn)) and \
+            x_flat.dtype in (torch.bfloat16, torch.float16) and self.num_experts() <= 512 and \
+            self.k <= min(32, self.num_experts()) and gu.group_size == dn.group_size and \
+            x_flat.shape[1] % 32 == 0 and x_flat.shape[1] <= 8192 and \
+            gu.weight.shape[1] % 64 == 0 and gu.weight.shape[1] // 2 <= 2048
+
+    def token_forward(self, x_flat, logits, stream=None):
+        gu, dn = self.experts["gate_up"], self.experts["down"]
+        return ops.moe_token(logits, x_flat.contiguous(), (gu.weight, gu.scales, gu.biases),
+                             (dn.weight, dn.scales, dn.biases), self.k, self.norm_topk_prob,
+                             gu.group_size, 4, stream)
+
     def __call__(self, x, stream=None):
         b, l, d = x.shape
         x_flat = x.reshape(b * l, d)
-        scores, idx = self.route(x_flat, stream)
-        out = self.experts_forward(x_flat, scores, idx, stream)
+        if self._token_path(x_flat):
+            out = self.token_forward(x_flat, self.gate(x_flat).contiguous(), stream)
+        else:
+            scores, idx = self.route(x_flat, stream)
+            out = self.experts_forward(x_flat, scores, idx, stream)
         shared = self.shared_expert(x_flat, stream)
         gate = torch.sigmoid(self.shared_expert_gate(x_flat))
         return (out + (shared * gate).float()).reshape(b, l, d)

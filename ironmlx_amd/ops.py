@@ -227,6 +227,21 @@ def moe_combine(y: torch.Tensor, inverse: torch.Tensor, experts: torch.Tensor,
     return _run(L.iqmm_moe_combine, _lib.IqmmArray(), dev, args)
 
 
+def moe_token(logits: torch.Tensor, x: torch.Tensor, gate_up, down, k: int,
+              norm_topk_prob: bool = True, group_size: int = 64, bits: int = 4,
+              stream=None) -> torch.Tensor:
+    """One token's routed experts (route, fused gate_up SwiGLU, down, ordered
+    combine; mlx/src/nn/moe.rs:55-183 for T = 1) in two launches.  ``gate_up``
+    and ``down`` are (weight, scales, biases) of the stacked affine 4-bit
+    experts.  Returns float32 [1, D]."""
+    L = _lib.load()
+    (gw, gs, gb), (dw, ds, db) = gate_up, down
+    dev = _device_of(logits, x, gw, gs, gb, dw, ds, db)
+    args = (_arr(logits), _arr(x), _arr(gw, True), _arr(gs), _arr(gb), _arr(dw, True), _arr(ds),
+            _arr(db), int(k), bool(norm_topk_prob), int(group_size), int(bits), _stream(dev, stream))
+    return _run(L.iqmm_moe_token, _lib.IqmmArray(), dev, args)
+
+
 def quantize(w: torch.Tensor, group_size: Optional[int] = None, bits: Optional[int] = None,
              mode: str = "affine", stream=None
              ) -> Tuple[torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:

@@ -54,10 +54,11 @@ def test_fused_qkv_matches_projections():
             assert ((got.float() - ref.float()).abs().max() / ref.float().abs().max()).item() <= 1e-2
 
 
-@pytest.mark.parametrize("T", [37, 2])
+@pytest.mark.parametrize("T", [37, 2, 1])
 @pytest.mark.parametrize("fused", [False, True])
 def test_moe_matches_per_expert_loop(fused, T):
-    # T = 2 (8 rows) skips the sort: one GEMV row per (token, slot)
+    # T = 2 (8 rows) skips the sort: one GEMV row per (token, slot); T = 1 with
+    # the fused gate_up experts runs the one-token kernels (ops.moe_token)
     torch.manual_seed(1)
     E, H, I, k = 16, 256, 128, 4
     dt = torch.bfloat16
