@@ -16,9 +16,10 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libiqmm.so")
-SOURCES = ["api.hip", "qmv.hip", "qmv_q4.hip", "qmm_mfma.hip", "qmm_gemm.hip", "qmm_skinny.hip", "convert.hip", "moe.hip", "workspace.hip", "qmm_decode.hip", "qmm_gather.hip"]
+SOURCES = ["api.hip", "qmv.hip", "qmv_q4.hip", "qmm_mfma.hip", "qmm_gemm.hip", "qmm_skinny.hip", "convert.hip", "moe.hip", "workspace.hip", "qmm_decode.hip", "qmm_gather.hip", "qmm_stream.hip"]
 # per-file flags: MFMA results in VGPRs (no AGPR round trip before the VALU epilogue)
-FILE_FLAGS = {"qmm_decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+FILE_FLAGS = {"qmm_decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+              "qmm_stream.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",

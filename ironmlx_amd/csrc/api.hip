@@ -204,6 +204,7 @@ hipError_t run_qmm(QmmArgs& a) {
   // decode widths on the MFMA decode kernel; M = 2 / 3 only for long K, where
   // the split-K skinny kernel is slow (N = 4096, K = 14336, M = 2: 20.4 us ->
   // the decode kernel's ~14 us at M = 4), while at K = 4096 it stays ahead
+  if (a.M >= 4 && qmm_stream_supported(a)) return launch_qmm_stream(a);
   if ((a.M >= 4 || a.K >= 8192) && qmm_decode_supported(a)) return launch_qmm_decode(a);
   if (a.nbatch <= 65535 && qmm_skinny_fac_supported(a)) return launch_qmm_skinny_fac(a);
   if (a.M >= 2 && a.M <= 64 && a.nbatch * ((a.M + 31) / 32) <= 65535 && qmm_skinny_supported(a))
@@ -228,6 +229,7 @@ template <class F>
 hipError_t run_glu(QmmArgs& a, bool try_fused, F&& product) {
   a.glu = 1;
   if (try_fused && qmv_q4_m1_supported(a)) return launch_qmv_q4_m1(a);
+  if (try_fused && a.M >= 4 && qmm_stream_supported(a)) return launch_qmm_stream(a);
   if (try_fused && a.M >= 2 && qmm_decode_supported(a)) return launch_qmm_decode(a);
   if (try_fused && a.nbatch <= 65535 && qmm_skinny_fac_supported(a)) return launch_qmm_skinny_fac(a);
   a.glu = 0;

@@ -88,6 +88,9 @@ hipError_t launch_moe_sort(const int32_t* experts, int n, int k, int E, int32_t*
 // the same sort with its bucket counts in a fixed per-device array (allocates nothing)
 hipError_t launch_moe_sort_noalloc(const int32_t* experts, int n, int k, int E, int32_t* tokens, int32_t* sorted,
                                    int32_t* inverse, int32_t* offsets, hipStream_t st);
+// decode widths on wide matrices, streaming tile-blocks per CU (qmm_stream.hip)
+bool qmm_stream_supported(const QmmArgs& a);
+hipError_t launch_qmm_stream(const QmmArgs& a);
 // one token's MoE experts (route + fused gate_up SwiGLU + down + combine),
 // affine 4-bit (moe.hip)
 bool moe_token_supported(int E, int k, int H, int I, int D, int gs);

@@ -153,3 +153,32 @@ def test_tied_lm_head_gemv_vs_oracle(ops):
     ref = oracle.qmv_affine(to_np(x, "bf16"), "bf16", _words(wq), to_np(s, "bf16"),
                             to_np(b, "bf16"), "bf16", 64, 4, odt="f32", nthreads=NT)
     assert rel_err(as_f64(to_np(got, "bf16"), "bf16"), ref) <= TOL_AFFINE
+
+
+@pytest.mark.parametrize("N,M", [(128256, 8), (65536, 20)])
+def test_wide_matrix_decode_widths_vs_oracle(ops, N, M):
+    """Wide matrices at decode widths (the tied lm_head at batched decode,
+    llama.rs:158-162): the streaming kernel, one and two m tiles."""
+    K = 4096
+    print(f"wide qmm M={M} N={N} K={K}", flush=True)
+    wq, s, b = _weight(ops, N, K, seed=N + M)
+    x = _x(M, K, seed=M + 1)
+    got = ops.quantized_matmul(x, wq, s, b, True, 64, 4)
+    ref = oracle.qmv_affine(to_np(x, "bf16"), "bf16", _words(wq), to_np(s, "bf16"),
+                            to_np(b, "bf16"), "bf16", 64, 4, odt="f32", nthreads=NT)
+    assert rel_err(as_f64(to_np(got, "bf16"), "bf16"), ref) <= TOL_AFFINE
+
+
+@pytest.mark.parametrize("gs,M,dt", [(32, 8, "bf16"), (64, 12, "f16")])
+def test_fused_swiglu_group_sizes_vs_oracle(ops, gs, M, dt):
+    """The streaming SwiGLU kernel at gs 32 and in fp16, I = 14336."""
+    I, K = 14336, 4096
+    tdt = torch.bfloat16 if dt == "bf16" else torch.float16
+    print(f"SwiGLU gs={gs} M={M} {dt}", flush=True)
+    wq, s, b = _weight(ops, 2 * I, K, seed=11 + gs, gs=gs, dt=tdt)
+    x = _x(M, K, seed=80 + M, dt=tdt)
+    got = ops.quantized_swiglu(x, wq, s, b, gs, 4)
+    gu = oracle.qmv_affine(to_np(x, dt), dt, _words(wq), to_np(s, dt), to_np(b, dt), dt, gs, 4,
+                           odt=dt, nthreads=NT)
+    ref = as_f64(oracle.swiglu(gu, dt), dt)
+    assert rel_err(as_f64(to_np(got, dt), dt), ref) <= TOL_AFFINE
