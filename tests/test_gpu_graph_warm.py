@@ -93,6 +93,25 @@ def test_graph_moe_block(ops, cap_stream):
     _check_warm_graph(block, cap_stream)
 
 
+def test_graph_moe_token_and_wide_decode(ops, cap_stream):
+    """The one-token MoE block (two launches, per-stream workspace for the
+    SwiGLU rows and the routing) and the streaming wide-matrix kernel
+    (N = 65536, M = 8) replayed from one graph."""
+    from ironmlx_amd import nn
+    gen = torch.Generator(device="cuda").manual_seed(26)
+    E, H, I, k = 256, 2048, 512, 8
+    experts = {"gate_up": nn.StackedExperts(*_weight(gen, (E,), 2 * I, H)),
+               "down": nn.StackedExperts(*_weight(gen, (E,), H, I))}
+    moe = nn.MoEMLP(None, experts, None, None, k, True)
+    logits = torch.randn((1, E), generator=gen, device="cuda").to(torch.bfloat16)
+    x1 = torch.randn((1, H), generator=gen, device="cuda").to(torch.bfloat16)
+    w, s, b = _weight(gen, (), 65536, 4096)
+    x8 = torch.randn((8, 4096), generator=gen, device="cuda").to(torch.bfloat16)
+    print("graph: one-token MoE block + wide decode N=65536 M=8", flush=True)
+    _check_warm_graph(lambda: (moe.token_forward(x1, logits), ops.quantized_matmul(x8, w, s, b, True, 64, 4)),
+                      cap_stream)
+
+
 def test_capture_on_unsized_stream_raises(ops):
     """Nothing is allocated during capture: on a stream whose split-K
     workspace was never sized, the captured call fails with a message (the
