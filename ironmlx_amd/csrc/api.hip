@@ -201,6 +201,7 @@ hipError_t fill_zero(void* p, int dt, int64_t n, hipStream_t st) {
 hipError_t run_qmm(QmmArgs& a) {
   if (qmv_q4_m1_supported(a)) return launch_qmv_q4_m1(a);
   if (qmv_q8_m1_supported(a)) return launch_qmv_q8_m1(a);
+  if (qmv_lb_m1_supported(a)) return launch_qmv_lb_m1(a);
   // decode widths on the MFMA decode kernel; M = 2 / 3 only for long K, where
   // the split-K skinny kernel is slow (N = 4096, K = 14336, M = 2: 20.4 us ->
   // the decode kernel's ~14 us at M = 4), while at K = 4096 it stays ahead

@@ -52,6 +52,8 @@ hipError_t launch_qmv_q4_m1(const QmmArgs& a);  // 4-bit affine M=1 decode fast 
 bool qmv_q4_m1_supported(const QmmArgs& a);
 hipError_t launch_qmv_q8_m1(const QmmArgs& a);  // 8-bit affine / mxfp8 M=1 decode path
 bool qmv_q8_m1_supported(const QmmArgs& a);
+hipError_t launch_qmv_lb_m1(const QmmArgs& a);  // affine 2 / 3 / 6-bit M=1 decode path
+bool qmv_lb_m1_supported(const QmmArgs& a);
 hipError_t launch_qvm(const QmmArgs& a);        // transpose=false, small M, VALU
 hipError_t launch_qmm_mfma(const QmmArgs& a);   // bf16/fp16 MFMA tiles, any M
 bool qmm_mfma_supported(const QmmArgs& a);

@@ -280,6 +280,119 @@ __attribute__((amdgpu_waves_per_eu(MR == 1 && RB == 2 && CPL == 2 && KS == 1 ? 7
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// M = 1 GEMV for affine 2-, 3- and 6-bit codes (transpose, one matrix).  Same
+// structure as qmv_q4_kernel: one wave per RB rows, lane l owns the 32-code
+// chunks l, l + 64, ... (BITS words each, LSB-first code stream), x chunk
+// loaded once for all rows, scale / bias per group, factored rescale
+// s (d - C xs) + b xs.  Codes become C + q halves without conversions:
+// 2-bit codes are spread one per byte by masks and placed by v_perm_b32
+// against the exponent bytes (as the 4-bit kernel does with nibbles), pairing
+// codes (k, 8 + k) and (4 + k, 12 + k) of each word with x permuted alike;
+// 3- and 6-bit codes (which straddle bytes and words) are cut with bitfield
+// extracts into natural pairs (2t, 2t + 1), which take the raw x dwords.
+template <int XT, int BITS, int RB, int CPL>
+__global__ __launch_bounds__(64) void qmv_lb_kernel(Q4Args p) {
+  static_assert(BITS == 2 || BITS == 3 || BITS == 6, "low-bit kernel");
+  using XS = uint16_t;
+  const int lane = threadIdx.x;
+  const int N = p.N, K = p.K, C = K >> 5;
+  XS* out = reinterpret_cast<XS*>(p.out);
+  const int row0 = blockIdx.x * RB;
+  const uint32_t wrow = static_cast<uint32_t>(K) / 8 * BITS;
+  const uint32_t srow = (static_cast<uint32_t>(K) >> p.gshift) * 2;
+  const uint32_t E = Magic<XT>::ebytes;
+  int cl[CPL];
+  uint32_t cidx[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    cl[j] = lane + 64 * j;
+    cidx[j] = static_cast<uint32_t>(min(cl[j], C - 1));
+  }
+  // x of each chunk: raw dwords (natural pairs) or the 2-bit pair order
+  uint32_t P[CPL][16];
+  float xs[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const u32x4_t* xc = reinterpret_cast<const u32x4_t*>(p.x + cidx[j] * 64);
+    uint32_t X[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const u32x4_t v = xc[i];
+      X[4 * i] = v.x; X[4 * i + 1] = v.y; X[4 * i + 2] = v.z; X[4 * i + 3] = v.w;
+    }
+    xs[j] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) xs[j] = dot2<XT>(X[i], Magic<XT>::one2, xs[j]);
+    if (cl[j] >= C) xs[j] = 0.f;
+    if constexpr (BITS == 2) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint32_t sel = (k & 1) ? 0x07060302u : 0x05040100u;
+          // pairs (16u + k, 16u + 8 + k) and (16u + 4 + k, 16u + 12 + k)
+          P[j][8 * u + 2 * k] = __builtin_amdgcn_perm(X[(16 * u + 8 + k) / 2], X[(16 * u + k) / 2], sel);
+          P[j][8 * u + 2 * k + 1] = __builtin_amdgcn_perm(X[(16 * u + 12 + k) / 2], X[(16 * u + 4 + k) / 2], sel);
+        }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) P[j][i] = X[i];
+    }
+  }
+  float red[RB];
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    const uint32_t row = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(min(row0 + r, N - 1)));
+    const char* wr = p.w + row * wrow;
+    const char* sr_ = p.s + row * srow;
+    const char* br_ = p.b + row * srow;
+    float acc = 0.f;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      uint32_t w[BITS];
+      const uint32_t* wc = reinterpret_cast<const uint32_t*>(wr + cidx[j] * (4 * BITS));
+#pragma unroll
+      for (int i = 0; i < BITS; ++i) w[i] = __builtin_nontemporal_load(wc + i);
+      const uint32_t g = ((cidx[j] << 5) >> p.gshift) * 2;
+      const float s = to_f<XT>(*reinterpret_cast<const XS*>(sr_ + g));
+      const float b = to_f<XT>(*reinterpret_cast<const XS*>(br_ + g));
+      float d = 0.f;
+      if constexpr (BITS == 2) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const uint32_t m = (w[u] >> (2 * k)) & 0x03030303u;  // codes 4 byte + k, one per byte
+            d = dot2<XT>(__builtin_amdgcn_perm(E, m, SEL_B0B2), P[j][8 * u + 2 * k], d);
+            d = dot2<XT>(__builtin_amdgcn_perm(E, m, SEL_B1B3), P[j][8 * u + 2 * k + 1], d);
+          }
+      } else {
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+          uint32_t c[2];
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int pos = BITS * (2 * t + h), wi = pos >> 5, bit = pos & 31;
+            c[h] = bit + BITS <= 32 ? __builtin_amdgcn_ubfe(w[wi], bit, BITS)
+                                    : __builtin_amdgcn_ubfe(__builtin_amdgcn_alignbit(w[wi + 1], w[wi], bit), 0, BITS);
+          }
+          d = dot2<XT>((c[1] << 16) | c[0] | (E & 0xFF00FF00u), P[j][t], d);
+        }
+      }
+      if (cl[j] >= C) d = 0.f;
+      acc = fmaf(s, fmaf(-Magic<XT>::c, xs[j], d), fmaf(b, xs[j], acc));
+    }
+    red[r] = dpp_sum_to_lane63(acc);
+  }
+  if (lane == 63) {
+#pragma unroll
+    for (int r = 0; r < RB; ++r)
+      if (row0 + r < N) out[row0 + r] = from_f<XT>(red[r]);
+  }
+}
+
 bool qmv_q4_m1_supported(const QmmArgs& a) {
   // K in [1024, 16384]: one to eight 32-code chunks per lane per row
   // one matrix's codes below 4 GiB: row offsets are 32-bit
@@ -501,6 +614,63 @@ __global__ __launch_bounds__(64) void qmv_q8_kernel(Q4Args p) {
     const float v = dpp_sum_to_lane63(acc);
     if (lane == 63 && row0 + r < N) out[row0 + r] = from_f<XT>(v);
   }
+}
+
+
+bool qmv_lb_m1_supported(const QmmArgs& a) {
+  // M = 1, affine 2 / 3 / 6-bit, K in [1024, 16384] (one to eight chunks per
+  // lane), one matrix below 4 GiB of codes
+  return a.transpose && a.M == 1 && !a.glu && a.mode == AFFINE && (a.bits == 2 || a.bits == 3 || a.bits == 6) &&
+         (a.xdt == BF16 || a.xdt == F16) && a.nbatch == 1 && a.bm.ndim == 0 && a.bm.lhs == nullptr &&
+         a.bm.rhs == nullptr && a.K % 32 == 0 && a.K >= 1024 && a.K <= 16384 &&
+         static_cast<int64_t>(a.N) * a.K / 8 * a.bits < (int64_t{1} << 32);
+}
+
+namespace {
+template <int XT, int BITS, int CPL>
+hipError_t lb_launch(const QmmArgs& a, const Q4Args& p) {
+  // two rows per wave from 4096 rows (as the 4-bit kernel), one below
+  if (a.N >= 4096) {
+    hipLaunchKernelGGL((qmv_lb_kernel<XT, BITS, 2, CPL>), dim3(static_cast<unsigned>((a.N + 1) / 2)), dim3(64), 0,
+                       a.stream, p);
+  } else {
+    hipLaunchKernelGGL((qmv_lb_kernel<XT, BITS, 1, CPL>), dim3(static_cast<unsigned>(a.N)), dim3(64), 0, a.stream, p);
+  }
+  return hipGetLastError();
+}
+template <int XT, int BITS>
+hipError_t lb_cpl(const QmmArgs& a, const Q4Args& p) {
+  switch (((a.K >> 5) + 63) / 64) {
+    case 1: return lb_launch<XT, BITS, 1>(a, p);
+    case 2: return lb_launch<XT, BITS, 2>(a, p);
+    case 3: return lb_launch<XT, BITS, 3>(a, p);
+    case 4: return lb_launch<XT, BITS, 4>(a, p);
+    case 5: case 6: return lb_launch<XT, BITS, 6>(a, p);
+    default: return lb_launch<XT, BITS, 8>(a, p);
+  }
+}
+template <int XT>
+hipError_t lb_bits(const QmmArgs& a, const Q4Args& p) {
+  if (a.bits == 2) return lb_cpl<XT, 2>(a, p);
+  if (a.bits == 3) return lb_cpl<XT, 3>(a, p);
+  return lb_cpl<XT, 6>(a, p);
+}
+}  // namespace
+
+hipError_t launch_qmv_lb_m1(const QmmArgs& a) {
+  if (a.N <= 0) return hipSuccess;
+  Q4Args p;
+  p.x = static_cast<const char*>(a.x);
+  p.w = reinterpret_cast<const char*>(a.w);
+  p.s = static_cast<const char*>(a.s);
+  p.b = static_cast<const char*>(a.b);
+  p.out = static_cast<char*>(a.out);
+  p.N = a.N;
+  p.K = a.K;
+  p.gshift = __builtin_ctz(a.gs);
+  p.pad = 0;
+  p.x_mat = p.w_mat = p.s_mat = 0;
+  return a.xdt == BF16 ? lb_bits<BF16>(a, p) : lb_bits<F16>(a, p);
 }
 
 bool qmv_q8_m1_supported(const QmmArgs& a) {

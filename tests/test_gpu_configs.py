@@ -182,3 +182,20 @@ def test_fused_swiglu_group_sizes_vs_oracle(ops, gs, M, dt):
                            odt=dt, nthreads=NT)
     ref = as_f64(oracle.swiglu(gu, dt), dt)
     assert rel_err(as_f64(to_np(got, dt), dt), ref) <= TOL_AFFINE
+
+
+@pytest.mark.parametrize("bits", [2, 3, 6])
+@pytest.mark.parametrize("N,K,gs,dt", [(1000, 1024, 32, "bf16"), (4097, 6144, 64, "f16"),
+                                       (4096, 14336, 128, "bf16"), (2047, 4096, 64, "f16")])
+def test_low_bit_gemv_widths_vs_oracle(ops, bits, N, K, gs, dt):
+    """The affine 2 / 3 / 6-bit one-row GEMV: one and two rows per wave (N
+    below / from 4096, with a ragged last pair), one to seven chunks per
+    lane, bf16 and fp16."""
+    print(f"low-bit GEMV bits={bits} N={N} K={K} gs={gs} {dt}", flush=True)
+    tdt = torch.bfloat16 if dt == "bf16" else torch.float16
+    wq, s, b = _weight(ops, N, K, seed=900 + bits + K, gs=gs, bits=bits, dt=tdt)
+    x = _x(1, K, seed=9, dt=tdt)
+    got = ops.quantized_matmul(x, wq, s, b, True, gs, bits)
+    ref = oracle.qmm(to_np(x, dt), dt, _words(wq), to_np(s, dt), to_np(b, dt),
+                     dt, True, gs, bits, "affine", odt="f32", nthreads=NT)
+    assert rel_err(as_f64(to_np(got, dt), dt), ref) <= TOL_AFFINE
