@@ -105,7 +105,7 @@ hipError_t launch_moe_combine(const void* y, int dt, const int32_t* inverse, con
 // Scratch of one call: the (device, stream, slot) buffer, grown outside
 // capture; during capture a request larger than the buffer fails with
 // hipErrorStreamCaptureUnsupported (nothing is allocated inside a graph).
-enum WsSlot : int { WS_SPLITK = 0, WS_GLU = 1, WS_OFFSETS = 2, WS_SORT = 3, WS_CONV = 4, WS_MOE = 5, WS_NSLOTS = 6 };
+enum WsSlot : int { WS_SPLITK = 0, WS_GLU = 1, WS_OFFSETS = 2, WS_SORT = 3, WS_CONV = 4, WS_MOE = 5, WS_CODES = 6, WS_NSLOTS = 7 };
 hipError_t workspace_get(hipStream_t st, int slot, size_t bytes, void** p);
 // grow every slot of the stream to at least `bytes` (outside capture)
 hipError_t workspace_reserve(hipStream_t st, size_t bytes);

@@ -956,6 +956,33 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* part, u
   }
 }
 
+// Widen packed affine codes to the register-B kernel's code widths: 2- and
+// 3-bit codes to 4-bit, 5- and 6-bit codes to 8-bit (codes, scales and biases
+// unchanged, so the product is the one the narrow codes define).  One thread
+// per 32-code chunk (BITS words of the LSB-first row stream in, 32 * OB bits
+// out); rows of K codes are whole chunks, so the matrix is one chunk sequence.
+template <int BITS, int OB>
+__global__ __launch_bounds__(256) void widen_codes_kernel(const uint32_t* __restrict__ w, uint32_t* __restrict__ o,
+                                                          int64_t nchunks) {
+  const int64_t c = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+  if (c >= nchunks) return;
+  uint32_t in[BITS + 1];
+#pragma unroll
+  for (int i = 0; i < BITS; ++i) in[i] = __builtin_nontemporal_load(w + c * BITS + i);
+  in[BITS] = 0;
+  uint32_t out[OB] = {};
+#pragma unroll
+  for (int n = 0; n < 32; ++n) {
+    const int pos = BITS * n, wi = pos >> 5, bit = pos & 31;
+    const uint32_t v = bit + BITS <= 32 ? __builtin_amdgcn_ubfe(in[wi], bit, BITS)
+                                        : __builtin_amdgcn_ubfe(__builtin_amdgcn_alignbit(in[wi + 1], in[wi], bit), 0, BITS);
+    out[(OB * n) >> 5] |= v << ((OB * n) & 31);
+  }
+  g_u32x4_t* dst = reinterpret_cast<g_u32x4_t*>(o + c * OB);
+#pragma unroll
+  for (int i = 0; i < OB / 4; ++i) dst[i] = g_u32x4_t{out[4 * i], out[4 * i + 1], out[4 * i + 2], out[4 * i + 3]};
+}
+
 template <int BITS, int MODE>
 constexpr size_t dma_lds_bytes() {
   return DEPTH * DA_STAGE * 2 + DEPTH * DmaCounts<BITS, MODE>::WBYTES + 2 * DEPTH * GBN * 4 +
@@ -1050,9 +1077,30 @@ hipError_t gemm_launch_t(const QmmArgs& a) {
   constexpr int GPC = MODE == AFFINE ? 8 : 16;
   const bool wr_ok = dma_ok && (BITS == 4 || BITS == 8) && a.K % (32 * (BITS == 4 ? 4 : 2)) == 0 &&
                      G % GPC == 0;
-  if (wr_ok) {
-    if constexpr (BITS == 4 || BITS == 8) return wr_launch<XT, MODE, BITS>(a, G);
-  } else if (dma_ok) {
+  if constexpr (BITS == 4 || BITS == 8) {
+    if (wr_ok) return wr_launch<XT, MODE, BITS>(a, G);
+  } else if constexpr (MODE == AFFINE) {
+    // 2 / 3 / 5 / 6-bit codes of one weight matrix: widen them into the
+    // stream's code workspace (N K / 2 or N K bytes) and run the register-B
+    // kernel on the wide codes
+    constexpr int OB = BITS < 4 ? 4 : 8;
+    const bool one_w = a.bm.ndim == 0 && a.bm.lhs == nullptr && a.bm.rhs == nullptr;
+    if (dma_ok && one_w && a.K % (32 * (OB == 4 ? 4 : 2)) == 0 && G % GPC == 0) {
+      const int64_t nchunks = static_cast<int64_t>(a.N) * (a.K / 32);
+      void* ws = nullptr;
+      hipError_t e = workspace_get(a.stream, WS_CODES, static_cast<size_t>(nchunks) * OB * 4, &ws);
+      if (e != hipSuccess) return e;
+      hipLaunchKernelGGL((widen_codes_kernel<BITS, OB>), dim3(static_cast<unsigned>((nchunks + 255) / 256)), dim3(256),
+                         0, a.stream, a.w, static_cast<uint32_t*>(ws), nchunks);
+      if ((e = hipGetLastError()) != hipSuccess) return e;
+      QmmArgs b = a;
+      b.w = static_cast<const uint32_t*>(ws);
+      b.bits = OB;
+      b.w_mat = nchunks * OB;
+      return wr_launch<XT, MODE, OB>(b, G);
+    }
+  }
+  if (dma_ok) {
     constexpr auto kern = qmm_gemm_dma8_kernel<XT, MODE, BITS>;
     constexpr size_t lds = dma_lds_bytes<BITS, MODE>();
     hipError_t e = set_lds_once<kern>(lds);

@@ -199,3 +199,18 @@ def test_low_bit_gemv_widths_vs_oracle(ops, bits, N, K, gs, dt):
     ref = oracle.qmm(to_np(x, dt), dt, _words(wq), to_np(s, dt), to_np(b, dt),
                      dt, True, gs, bits, "affine", odt="f32", nthreads=NT)
     assert rel_err(as_f64(to_np(got, dt), dt), ref) <= TOL_AFFINE
+
+
+@pytest.mark.parametrize("bits", [2, 3, 5, 6])
+@pytest.mark.parametrize("M,N,K,gs,dt", [(130, 1000, 1024, 32, "f16"), (300, 4096, 2048, 128, "bf16")])
+def test_widened_code_gemm_vs_oracle(ops, bits, M, N, K, gs, dt):
+    """M > 64 with 2 / 3 / 5 / 6-bit codes: the codes are widened to 4 or 8
+    bits in the stream's workspace and run through the register-B GEMM."""
+    print(f"widened GEMM bits={bits} M={M} N={N} K={K} gs={gs} {dt}", flush=True)
+    tdt = torch.bfloat16 if dt == "bf16" else torch.float16
+    wq, s, b = _weight(ops, N, K, seed=950 + bits + M, gs=gs, bits=bits, dt=tdt)
+    x = _x(M, K, seed=11, dt=tdt)
+    got = ops.quantized_matmul(x, wq, s, b, True, gs, bits)
+    ref = oracle.qmm(to_np(x, dt), dt, _words(wq), to_np(s, dt), to_np(b, dt),
+                     dt, True, gs, bits, "affine", odt="f32", nthreads=NT)
+    assert rel_err(as_f64(to_np(got, dt), dt), ref) <= TOL_AFFINE
