@@ -42,8 +42,9 @@
  * stream is synchronised, as after mlx's `eval` (mlx/src/array.rs:111-113).
  * Scratch memory: the fp32 partial sums of a split-K GEMM (few output tiles,
  * M > 64), the gate_up product of a fused SwiGLU outside its fused kernels,
- * the expert segment offsets of a sorted grouped gather_qmm and the per-block
- * bucket counts of iqmm_moe_sort live in per-stream workspaces: one
+ * the expert segment offsets of a sorted grouped gather_qmm, the per-block
+ * bucket counts of iqmm_moe_sort and the widened codes of a 2 / 3 / 5 / 6-bit
+ * weight at M > 64 (N K / 2 or N K bytes) live in per-stream workspaces: one
  * grow-only buffer per (device, stream, use), taken from the stream-ordered
  * pool (hipMallocAsync on `stream`) and kept until the process ends, so HIP
  * graphs captured on a stream keep valid pointers and hold kernel nodes only.
