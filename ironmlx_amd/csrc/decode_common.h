@@ -47,24 +47,14 @@ __device__ __forceinline__ g_u32x4_t x_pairs(const g_u32x4_t& v) {
                    __builtin_amdgcn_perm(v.w, v.y, 0x05040100u), __builtin_amdgcn_perm(v.w, v.y, 0x07060302u)};
 }
 
-// One 128-code block of the factored affine 4-bit product for NT 16-row
-// weight tiles and MT 16-row x tiles.  A holds the x operands (x_pairs) of
-// the block's four 32-code MFMA slots; the weights are the block's 64-byte
-// row pieces in LDS at wst + row * 128 + 16 * ((4 h + q) ^ (row & 7)) (h: the
-// block's half of a two-block stage, pieces XOR-swizzled by the row); sw / bw
-// hold the scale / bias halves of the wave's K range, hb the first half of
-// this block.  Y[tt][i] accumulates sum_g s D + (b - C s) X.
-template <int XT, int NT, int MT, int GB, int SW>
-__device__ __forceinline__ void fac_block(f32x4d_t (&Y)[NT][MT], const g_u32x4_t (&A)[MT][4], const char* wst, int h,
-                                          int hb, const uint32_t (&sw)[NT][SW], const uint32_t (&bw)[NT][SW], int r,
-                                          int q) {
-  using XS = uint16_t;
-  constexpr float CM = XT == BF16 ? 128.f : 1024.f;
-  constexpr uint32_t EB = XT == BF16 ? 0x43434343u : 0x64646464u;
+// The group sums X of one block: XG[i][g] holds, in the MFMA output layout,
+// sum x over group g of the block for the rows of m tile i (every column
+// equal), computed by MFMAs against a B operand of ones.
+template <int XT, int MT, int GB>
+__device__ __forceinline__ void block_xsums(f32x4d_t (&XG)[MT][GB], const g_u32x4_t (&A)[MT][4]) {
   constexpr uint32_t ONE2 = XT == BF16 ? 0x3f803f80u : 0x3c003c00u;
   constexpr int JG = 4 / GB;  // MFMAs per group
   const g_u32x4_t ones = {ONE2, ONE2, ONE2, ONE2};
-  f32x4d_t XG[MT][GB];
 #pragma unroll
   for (int i = 0; i < MT; ++i)
 #pragma unroll
@@ -73,6 +63,27 @@ __device__ __forceinline__ void fac_block(f32x4d_t (&Y)[NT][MT], const g_u32x4_t
 #pragma unroll
       for (int j = 1; j < JG; ++j) XG[i][g] = mfma16<XT>(A[i][g * JG + j], ones, XG[i][g]);
     }
+}
+
+// One 128-code block of the factored affine 4-bit product for NT 16-row
+// weight tiles and MT 16-row x tiles.  A holds the x operands (x_pairs) of
+// the block's four 32-code MFMA slots; the weights are the block's 64-byte
+// row pieces in LDS at wst + row * 128 + 16 * ((4 h + q) ^ (row & 7)) (h: the
+// block's half of a two-block stage, pieces XOR-swizzled by the row); sw / bw
+// hold the scale / bias halves of the wave's K range, hb the first half of
+// this block.  Y[tt][i] accumulates sum_g s D + (b - C s) X.
+// fac_block_xs takes the block's group sums already computed (block_xsums),
+// for kernels that reuse one x block against many weight tiles; fac_block
+// computes them itself.
+template <int XT, int NT, int MT, int GB, int SW>
+__device__ __forceinline__ void fac_block_xs(f32x4d_t (&Y)[NT][MT], const g_u32x4_t (&A)[MT][4],
+                                             const f32x4d_t (&XG)[MT][GB], const char* wst, int h, int hb,
+                                             const uint32_t (&sw)[NT][SW], const uint32_t (&bw)[NT][SW], int r,
+                                             int q) {
+  using XS = uint16_t;
+  constexpr float CM = XT == BF16 ? 128.f : 1024.f;
+  constexpr uint32_t EB = XT == BF16 ? 0x43434343u : 0x64646464u;
+  constexpr int JG = 4 / GB;  // MFMAs per group
 #pragma unroll
   for (int tt = 0; tt < NT; ++tt) {
     const int row = 16 * tt + r;
@@ -108,6 +119,15 @@ __device__ __forceinline__ void fac_block(f32x4d_t (&Y)[NT][MT], const g_u32x4_t
       }
     }
   }
+}
+
+template <int XT, int NT, int MT, int GB, int SW>
+__device__ __forceinline__ void fac_block(f32x4d_t (&Y)[NT][MT], const g_u32x4_t (&A)[MT][4], const char* wst, int h,
+                                          int hb, const uint32_t (&sw)[NT][SW], const uint32_t (&bw)[NT][SW], int r,
+                                          int q) {
+  f32x4d_t XG[MT][GB];
+  block_xsums<XT, MT, GB>(XG, A);
+  fac_block_xs<XT, NT, MT, GB, SW>(Y, A, XG, wst, h, hb, sw, bw, r, q);
 }
 
 }  // namespace iqmm

@@ -7,8 +7,8 @@
 // v_mfma_f32_16x16x32 as C + n halves, per-group rescale s D + (b - C s) X),
 // organised to overlap loads with compute.  A workgroup of S waves splits K
 // into S ranges of KB 128-code blocks; each wave loads the x fragments of its
-// range for all M rows ONCE, permuted into MFMA A operands held in registers,
-// and then streams a sequence of tile-blocks (NT 16-row weight tiles; a gate
+// range for all M rows ONCE, permuted into MFMA A operands held in registers
+// (with their per-group sums, where the registers allow), and then streams a sequence of tile-blocks (NT 16-row weight tiles; a gate
 // tile and its up tile for the SwiGLU) through a ring of D stages in its own
 // slice of LDS, filled by LDS DMA (8 rows x 128 B per instruction, pieces
 // XOR-swizzled by the row); each tile-block's scale and bias words come with
@@ -83,6 +83,15 @@ __global__ __launch_bounds__(64 * S) void qmm_stream_kernel(QmmArgs a, int ntb) 
   }
   // the compiler's own loads are complete before the counted DMA starts
   __builtin_amdgcn_s_waitcnt(0);
+  // group sums of the wave's x blocks, the same for every tile-block: kept in
+  // registers where they fit (one m tile at gs 64 / 128), else recomputed
+  // per tile-block by fac_block
+  constexpr bool PRE = MT * GB <= 2;
+  f32x4d_t XS_[PRE ? KB : 1][MT][GB];
+  if constexpr (PRE) {
+#pragma unroll
+    for (int b = 0; b < KB; ++b) block_xsums<XT, MT, GB>(XS_[b], A[b]);
+  }
 
   const int G = gridDim.x;
   const int nit = (ntb - static_cast<int>(blockIdx.x) + G - 1) / G;  // >= 1: G <= ntb
@@ -158,7 +167,12 @@ __global__ __launch_bounds__(64 * S) void qmm_stream_kernel(QmmArgs a, int ntb) 
       }
       const char* wst = lds_w + (u % D) * L::WST;
 #pragma unroll
-      for (int h = 0; h < 2; ++h) fac_block<XT, NT, MT, GB, SW>(Y, A[2 * st + h], wst, h, (2 * st + h) * GB, sw, bw, r, q);
+      for (int h = 0; h < 2; ++h) {
+        if constexpr (PRE)
+          fac_block_xs<XT, NT, MT, GB, SW>(Y, A[2 * st + h], XS_[2 * st + h], wst, h, (2 * st + h) * GB, sw, bw, r, q);
+        else
+          fac_block<XT, NT, MT, GB, SW>(Y, A[2 * st + h], wst, h, (2 * st + h) * GB, sw, bw, r, q);
+      }
     }
     // the S partial sums of tile-block it meet in LDS
     const int n0 = (static_cast<int>(blockIdx.x) + G * it) * NC;
@@ -241,13 +255,15 @@ bool qmm_stream_supported(const QmmArgs& a) {
          (reinterpret_cast<uintptr_t>(a.s) | reinterpret_cast<uintptr_t>(a.b)) % 16 == 0 && a.b != nullptr &&
          // two m tiles of the SwiGLU or of gs 32 exceed the register file
          !(a.M > 16 && (a.glu || a.gs == 32)) &&
-         // measured on MI355X (bf16, gs 64, K = 4096): ahead of the decode-width
-         // kernel where each CU streams several large tile-blocks -- the fused
-         // gate_up SwiGLU (2 x 14336 rows, M = 4 / 16: 21.7 / 24.3 -> 19.2 /
-         // 21.3 us) and very wide matrices (N = 128256, M = 8: 87.5 -> 66.0 us);
-         // equal or behind at N = 14336 and below (gate / up M = 16: 13.9 vs
-         // 14.2 us), which keep the decode-width kernel
-         (a.glu || static_cast<int64_t>(a.N) >= 65536);
+         // measured on MI355X (bf16, gs 64, K = 4096, group sums of x kept in
+         // registers): ahead of the decode-width kernel where each CU streams
+         // several tile-blocks -- the fused gate_up SwiGLU (2 x 14336 rows,
+         // M = 4 / 16: 21.7 / 24.3 -> 18.9 / 20.9 us), very wide matrices
+         // (N = 128256, M = 8: 87.5 -> 63.6 us), and 6144 .. 14336 rows at
+         // M <= 12 (N = 14336, M = 8: 12.4 -> 11.7 us; N = 10240, M = 4:
+         // 10.8 -> 9.1 us), also M = 16 from 10240 rows (N = 10240: 12.7 ->
+         // 11.5 us); behind at 6144 rows and M = 16 (8.5 vs 9.5 us)
+         (a.glu || static_cast<int64_t>(a.N) >= 65536 || (a.N >= 6144 && (a.M <= 12 || a.N >= 10240)));
 }
 
 hipError_t launch_qmm_stream(const QmmArgs& a) {

@@ -214,3 +214,18 @@ def test_widened_code_gemm_vs_oracle(ops, bits, M, N, K, gs, dt):
     ref = oracle.qmm(to_np(x, dt), dt, _words(wq), to_np(s, dt), to_np(b, dt),
                      dt, True, gs, bits, "affine", odt="f32", nthreads=NT)
     assert rel_err(as_f64(to_np(got, dt), dt), ref) <= TOL_AFFINE
+
+
+@pytest.mark.parametrize("N,M,gs,dt", [(10240, 16, 32, "f16"), (6144, 5, 64, "bf16"), (8000, 12, 64, "bf16"),
+                                       (6150, 9, 32, "bf16")])
+def test_streaming_decode_widths_vs_oracle(ops, N, M, gs, dt):
+    """The streaming kernel at 6144 .. 14336 rows (K = 4096): gs 32 / 64,
+    fp16, a ragged last tile, M not a multiple of 4."""
+    print(f"stream decode N={N} M={M} gs={gs} {dt}", flush=True)
+    tdt = torch.bfloat16 if dt == "bf16" else torch.float16
+    wq, s, b = _weight(ops, N, 4096, seed=970 + M, gs=gs, dt=tdt)
+    x = _x(M, 4096, seed=12, dt=tdt)
+    got = ops.quantized_matmul(x, wq, s, b, True, gs, 4)
+    ref = oracle.qmm(to_np(x, dt), dt, _words(wq), to_np(s, dt), to_np(b, dt),
+                     dt, True, gs, 4, "affine", odt="f32", nthreads=NT)
+    assert rel_err(as_f64(to_np(got, dt), dt), ref) <= TOL_AFFINE
