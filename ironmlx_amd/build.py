@@ -19,7 +19,8 @@ LIB = os.path.join(HERE, "libiqmm.so")
 SOURCES = ["api.hip", "qmv.hip", "qmv_q4.hip", "qmm_mfma.hip", "qmm_gemm.hip", "qmm_skinny.hip", "convert.hip", "moe.hip", "workspace.hip", "qmm_decode.hip", "qmm_gather.hip", "qmm_stream.hip"]
 # per-file flags: MFMA results in VGPRs (no AGPR round trip before the VALU epilogue)
 FILE_FLAGS = {"qmm_decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
-              "qmm_stream.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+              "qmm_stream.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+              "qmm_gather.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
