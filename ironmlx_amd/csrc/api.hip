@@ -199,6 +199,10 @@ hipError_t fill_zero(void* p, int dt, int64_t n, hipStream_t st) {
 
 // choose the kernel family for one problem
 hipError_t run_qmm(QmmArgs& a) {
+  // M = 2 / 3 on wide matrices: the streaming MFMA kernel is ahead of the
+  // multi-row GEMV (K = 4096: N = 14336, M = 2 / 3: 13.1 / 17.1 -> 10.9 /
+  // 10.9 us; N = 6144, M = 3: 8.6 -> 7.2 us; not at N = 6144, M = 2)
+  if (a.M >= 2 && a.M <= 3 && (a.M == 3 || a.N >= 10240) && qmm_stream_supported(a)) return launch_qmm_stream(a);
   if (qmv_q4_m1_supported(a)) return launch_qmv_q4_m1(a);
   if (qmv_q8_m1_supported(a)) return launch_qmv_q8_m1(a);
   if (qmv_lb_m1_supported(a)) return launch_qmv_lb_m1(a);
@@ -230,7 +234,8 @@ template <class F>
 hipError_t run_glu(QmmArgs& a, bool try_fused, F&& product) {
   a.glu = 1;
   if (try_fused && qmv_q4_m1_supported(a)) return launch_qmv_q4_m1(a);
-  if (try_fused && a.M >= 4 && qmm_stream_supported(a)) return launch_qmm_stream(a);
+  // (M = 2 / 3 at 2 x 14336 rows: 22.1 -> 19.3 us against the decode kernel)
+  if (try_fused && a.M >= 2 && qmm_stream_supported(a)) return launch_qmm_stream(a);
   if (try_fused && a.M >= 2 && qmm_decode_supported(a)) return launch_qmm_decode(a);
   if (try_fused && a.nbatch <= 65535 && qmm_skinny_fac_supported(a)) return launch_qmm_skinny_fac(a);
   a.glu = 0;

@@ -56,7 +56,7 @@ def _x(M, K, seed, dt=torch.bfloat16):
 C3_SHAPES = [(4096, 4096), (1024, 4096), (6144, 4096), (14336, 4096), (4096, 14336)]
 
 
-@pytest.mark.parametrize("M", [4, 8, 16, 32])
+@pytest.mark.parametrize("M", [2, 3, 4, 8, 16, 32])
 @pytest.mark.parametrize("N,K", C3_SHAPES)
 def test_llama_decode_widths_vs_oracle(ops, M, N, K):
     print(f"C3 qmm M={M} N={N} K={K}", flush=True)
@@ -68,7 +68,7 @@ def test_llama_decode_widths_vs_oracle(ops, M, N, K):
     assert rel_err(as_f64(to_np(got, "bf16"), "bf16"), ref) <= TOL_AFFINE
 
 
-@pytest.mark.parametrize("M", [1, 4, 16, 32])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 16, 32])
 def test_fused_swiglu_llama_vs_oracle(ops, M):
     """silu(x @ gate^T) * (x @ up^T) over the stacked [2I, K] gate_up weight,
     I = 14336: the oracle computes both products from the packed words,
@@ -169,7 +169,7 @@ def test_wide_matrix_decode_widths_vs_oracle(ops, N, M):
     assert rel_err(as_f64(to_np(got, "bf16"), "bf16"), ref) <= TOL_AFFINE
 
 
-@pytest.mark.parametrize("gs,M,dt", [(32, 8, "bf16"), (64, 12, "f16")])
+@pytest.mark.parametrize("gs,M,dt", [(32, 8, "bf16"), (64, 12, "f16"), (32, 3, "f16")])
 def test_fused_swiglu_group_sizes_vs_oracle(ops, gs, M, dt):
     """The streaming SwiGLU kernel at gs 32 and in fp16, I = 14336."""
     I, K = 14336, 4096
@@ -217,7 +217,7 @@ def test_widened_code_gemm_vs_oracle(ops, bits, M, N, K, gs, dt):
 
 
 @pytest.mark.parametrize("N,M,gs,dt", [(10240, 16, 32, "f16"), (6144, 5, 64, "bf16"), (8000, 12, 64, "bf16"),
-                                       (6150, 9, 32, "bf16")])
+                                       (6150, 9, 32, "bf16"), (10250, 2, 32, "f16"), (6144, 3, 64, "f16")])
 def test_streaming_decode_widths_vs_oracle(ops, N, M, gs, dt):
     """The streaming kernel at 6144 .. 14336 rows (K = 4096): gs 32 / 64,
     fp16, a ragged last tile, M not a multiple of 4."""
