@@ -261,9 +261,9 @@ bool qmm_stream_supported(const QmmArgs& a) {
          // M = 4 / 16: 21.7 / 24.3 -> 18.9 / 20.9 us), very wide matrices
          // (N = 128256, M = 8: 87.5 -> 63.6 us), and 6144 .. 14336 rows at
          // M <= 12 (N = 14336, M = 8: 12.4 -> 11.7 us; N = 10240, M = 4:
-         // 10.8 -> 9.1 us), also M = 16 from 10240 rows (N = 10240: 12.7 ->
-         // 11.5 us); behind at 6144 rows and M = 16 (8.5 vs 9.5 us)
-         (a.glu || static_cast<int64_t>(a.N) >= 65536 || (a.N >= 6144 && (a.M <= 12 || a.N >= 10240)));
+         // 10.8 -> 9.1 us); at M = 16 behind or even at 6144 and 14336 rows
+         // (8.5 vs 9.5 us; kernel average 13.1 vs 13.5 us)
+         (a.glu || static_cast<int64_t>(a.N) >= 65536 || (a.N >= 6144 && a.M <= 12));
 }
 
 hipError_t launch_qmm_stream(const QmmArgs& a) {
