@@ -52,7 +52,8 @@ def _float_probe(n=20000, seed=0):
 def test_half_encode_rne():
     v = _float_probe()
     got = oracle.from_float(v, "f16").view(np.uint16)
-    ref = v.astype(np.float16).view(np.uint16)
+    with np.errstate(over="ignore"):  # the probe holds values past fp16's range (-> inf)
+        ref = v.astype(np.float16).view(np.uint16)
     assert np.array_equal(got, ref)
 
 
