@@ -67,12 +67,12 @@ def time_launches(fn, n, stream):
     return sum(a.elapsed_time(b) for a, b in evs) / n * 1e-3
 
 
-def bench_gemv(ops, steps, warmup, M=1, N=14336, K=4096, pool_bytes=640 << 20):
+def bench_gemv(ops, steps, warmup, M=1, N=14336, K=4096, pool_bytes=640 << 20, dt=torch.bfloat16):
     gen = torch.Generator(device="cuda").manual_seed(0)
     per = gemv_bytes(M, N, K)
     P = max(2, int(np.ceil(pool_bytes / per)))
-    pool = [make_weight(ops, N, K, gen) for _ in range(P)]
-    x = torch.randn((M, K), generator=gen, device="cuda").to(torch.bfloat16)
+    pool = [make_weight(ops, N, K, gen, dt=dt) for _ in range(P)]
+    x = torch.randn((M, K), generator=gen, device="cuda").to(dt)
     stream = torch.cuda.current_stream()
     outs = [None] * P
 
@@ -631,6 +631,9 @@ def main():
     # tied lm_head of Llama-3-8B (LinearLayer::from_weights on model.embed_tokens,
     # mlx/src/model/llama.rs:158-162): the largest GEMV of a decode step
     lmh = bench_gemv(ops, max(3, args.steps // 4), args.warmup, M=1, N=128256, K=4096)
+    # configs[0]'s shape on the GPU (the reference's own CPU case): fp16 x and
+    # scales, N = 11008
+    c1 = bench_gemv(ops, args.steps, args.warmup, M=1, N=11008, K=4096, dt=torch.float16)
     tr = load_traffic()
     traffic = tr.get("gemv_q4_gs64_k4096_n14336_m1", {}).get("traffic_bytes")
     traffic_pf = tr.get("prefill_q4_gs64_m2048_k4096_n14336", {}).get("traffic_bytes")
@@ -674,6 +677,10 @@ def main():
                                           "gbs": round(lmh["kernel_gbs"], 1),
                                           "hbm_frac": round(lmh["kernel_gbs"] / HBM_PEAK_GBS, 4),
                                           "bytes_per_launch": lmh["bytes_per_launch"]},
+        "c1_gemv_fp16_n11008_k4096_m1": {"us": round(c1["avg_launch_us"], 2),
+                                         "gbs": round(c1["kernel_gbs"], 1),
+                                         "hbm_frac": round(c1["kernel_gbs"] / HBM_PEAK_GBS, 4),
+                                         "bytes_per_launch": c1["bytes_per_launch"]},
         "fused_paths": fused,
     }
     if sweep is not None:
