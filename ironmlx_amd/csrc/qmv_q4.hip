@@ -82,11 +82,21 @@ struct Q4Args {
 // KS > 1 (long K): the workgroup's KS waves split each row's chunks -- lane l
 // of wave w owns chunks l + 64 (w + KS j) -- and their row sums meet in LDS,
 // added in wave order.
-template <int XT, int RB, int CPL, bool MAPPED, int MR, int MODE = AFFINE, bool GLU = false, int KS = 1>
-__global__ __launch_bounds__(64 * KS)
+//
+// WG > 1 (M = 1, KS = 1): WG waves per workgroup, each with its own RB rows,
+// share one copy of x through LDS.  Every wave needs all of x (lane l reads
+// the x of chunks l, l + 64, ...), so with one wave per workgroup the x
+// reloads (K * 2 bytes per wave) outweigh the wave's weight bytes (RB * K / 2)
+// in each CU's vector-memory pipeline; here the workgroup loads x once
+// (issued first, before the weight loads), stores it piece-major in LDS
+// (piece i of chunk c at [i][c], so the lanes' reads are contiguous) and the
+// waves read their x chunks from LDS after one barrier.
+template <int XT, int RB, int CPL, bool MAPPED, int MR, int MODE = AFFINE, bool GLU = false, int KS = 1, int WG = 1>
+__global__ __launch_bounds__(64 * KS * WG)
 __attribute__((amdgpu_waves_per_eu(MR == 1 && RB == 2 && CPL == 2 && KS == 1 ? 7 : 1))) void qmv_q4_kernel(
     Q4Args p, BatchMap bm, int64_t batch0) {
   static_assert(!GLU || (MR == 1 && RB % 2 == 0), "GLU pairs gate / up rows at M = 1");
+  static_assert(WG == 1 || (KS == 1 && MR == 1 && (4 * CPL) % WG == 0), "shared x: one row of x, no K split");
   constexpr int RO = GLU ? RB / 2 : RB;  // outputs per wave
   using XS = uint16_t;
   const int lane = threadIdx.x & 63;
@@ -94,7 +104,8 @@ __attribute__((amdgpu_waves_per_eu(MR == 1 && RB == 2 && CPL == 2 && KS == 1 ? 7
   const int64_t bb = batch0 + blockIdx.y;
   const int N = p.N, K = p.K, C = K >> 5;
   XS* out = reinterpret_cast<XS*>(p.out) + bb * static_cast<int64_t>(N) * MR;
-  const int row0 = blockIdx.x * RO;
+  const int wv_id = WG > 1 ? __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6)) : 0;
+  const int row0 = (blockIdx.x * WG + wv_id) * RO;
 
   int64_t xi = bb, wi = bb;
   if constexpr (MAPPED) {
@@ -129,15 +140,26 @@ __attribute__((amdgpu_waves_per_eu(MR == 1 && RB == 2 && CPL == 2 && KS == 1 ? 7
     cg[j] = MODE == AFFINE ? ((cidx << 5) >> p.gshift) * 2 : MODE == MXFP4 ? cidx : 2 * cidx;
   }
 
-  // 1. x chunks (cache-resident) first
+  // 1. x chunks (cache-resident) first: each lane's own, or (WG > 1) this
+  //    thread's share of the workgroup's one copy
   u32x4_t xv[MR][CPL][4];
+  constexpr int XSH = WG > 1 ? 4 * CPL / WG : 1;  // 16-byte x pieces per thread
+  u32x4_t xsh[XSH];
+  if constexpr (WG > 1) {
 #pragma unroll
-  for (int m = 0; m < MR; ++m)
+    for (int u = 0; u < XSH; ++u) {
+      const int v = static_cast<int>(threadIdx.x) + 64 * WG * u;  // piece v % 4 of chunk v / 4
+      xsh[u] = *reinterpret_cast<const u32x4_t*>(xbase + min(v, 4 * C - 1) * 16);
+    }
+  } else {
 #pragma unroll
-    for (int j = 0; j < CPL; ++j)
+    for (int m = 0; m < MR; ++m)
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        xv[m][j][i] = *reinterpret_cast<const u32x4_t*>(xbase + m * xrow + cx[j] + 16 * i);
+      for (int j = 0; j < CPL; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          xv[m][j][i] = *reinterpret_cast<const u32x4_t*>(xbase + m * xrow + cx[j] + 16 * i);
+  }
   // 2. per row: weight chunks, then that row's scales / biases (row bases are
   //    wave-uniform, so every load is scalar base + 32-bit lane offset)
   u32x4_t wv[RB][CPL];
@@ -166,6 +188,19 @@ __attribute__((amdgpu_waves_per_eu(MR == 1 && RB == 2 && CPL == 2 && KS == 1 ? 7
     }
   }
   __builtin_amdgcn_sched_barrier(0);
+  if constexpr (WG > 1) {
+    __shared__ u32x4_t xl[4][64 * CPL];
+#pragma unroll
+    for (int u = 0; u < XSH; ++u) {
+      const int v = static_cast<int>(threadIdx.x) + 64 * WG * u;
+      xl[v & 3][v >> 2] = xsh[u];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < CPL; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) xv[0][j][i] = xl[i][cx[j] >> 6];
+  }
   // 3. x pairs and chunk sums (overlaps the weight loads)
   uint32_t P[MR][CPL][16];
   float xs[MR][CPL];
@@ -410,15 +445,15 @@ bool qmv_q4_m1_supported(const QmmArgs& a) {
 }
 
 namespace {
-template <int XT, int RB, int CPL, int MR, int MODE = AFFINE, bool GLU = false, int KS = 1>
+template <int XT, int RB, int CPL, int MR, int MODE = AFFINE, bool GLU = false, int KS = 1, int WG = 1>
 void launch_mr(dim3 grid, const QmmArgs& a, const Q4Args& p, bool mapped, int64_t b0) {
   if constexpr (MR * CPL * KS > 8 || (GLU && (MR != 1 || RB % 2 != 0))) return;  // excluded by the callers
   else if (mapped)
     hipLaunchKernelGGL((qmv_q4_kernel<XT, RB, CPL, true, MR, MODE, GLU, KS>), grid, dim3(64 * KS), 0, a.stream, p,
                        a.bm, b0);
   else
-    hipLaunchKernelGGL((qmv_q4_kernel<XT, RB, CPL, false, MR, MODE, GLU, KS>), grid, dim3(64 * KS), 0, a.stream, p,
-                       a.bm, b0);
+    hipLaunchKernelGGL((qmv_q4_kernel<XT, RB, CPL, false, MR, MODE, GLU, KS, WG>), dim3((grid.x + WG - 1) / WG, grid.y),
+                       dim3(64 * KS * WG), 0, a.stream, p, a.bm, b0);
 }
 
 template <int XT, int RB, int CPL, int KS = 1>
@@ -451,6 +486,15 @@ hipError_t launch_ord(const QmmArgs& a) {
     }
     if (a.mode == MXFP4) { launch_mr<XT, RB, CPL, 1, MXFP4, false, KS>(grid, a, p, mapped, b0); continue; }
     if (a.mode == NVFP4) { launch_mr<XT, RB, CPL, 1, NVFP4, false, KS>(grid, a, p, mapped, b0); continue; }
+    // four waves sharing x through LDS (measured, K = 4096, two rows per
+    // wave: N = 11008 / 14336 / 20480: 7.5 / 8.9 / 11.8 -> 7.2 / 8.3 / 10.5 us;
+    // even at 8192 rows, behind at 6144 and for the SwiGLU rows)
+    if constexpr (KS == 1 && RB == 2 && CPL == 2) {
+      if (a.M == 1 && !mapped && a.N >= 10240) {
+        launch_mr<XT, RB, CPL, 1, AFFINE, false, KS, 4>(grid, a, p, mapped, b0);
+        continue;
+      }
+    }
     switch (a.M) {
       case 1: launch_mr<XT, RB, CPL, 1, AFFINE, false, KS>(grid, a, p, mapped, b0); break;
       case 2: launch_mr<XT, RB, CPL, 2, AFFINE, false, KS>(grid, a, p, mapped, b0); break;

@@ -229,3 +229,18 @@ def test_streaming_decode_widths_vs_oracle(ops, N, M, gs, dt):
     ref = oracle.qmm(to_np(x, dt), dt, _words(wq), to_np(s, dt), to_np(b, dt),
                      dt, True, gs, 4, "affine", odt="f32", nthreads=NT)
     assert rel_err(as_f64(to_np(got, dt), dt), ref) <= TOL_AFFINE
+
+
+@pytest.mark.parametrize("N,K,dt", [(10250, 4096, "f16"), (20482, 4096, "bf16"), (12000, 3072, "bf16")])
+def test_shared_x_gemv_vs_oracle(ops, N, K, dt):
+    """The one-row GEMV with four waves sharing x through LDS (from 10240
+    rows): a ragged last workgroup (rows past N) and a K that leaves some
+    lanes' chunks masked."""
+    print(f"shared-x GEMV N={N} K={K} {dt}", flush=True)
+    tdt = torch.bfloat16 if dt == "bf16" else torch.float16
+    wq, s, b = _weight(ops, N, K, seed=990 + N % 97, gs=64, dt=tdt)
+    x = _x(1, K, seed=13, dt=tdt)
+    got = ops.quantized_matmul(x, wq, s, b, True, 64, 4)
+    ref = oracle.qmv_affine(to_np(x, dt), dt, _words(wq), to_np(s, dt), to_np(b, dt), dt, 64, 4,
+                            odt="f32", nthreads=NT)
+    assert rel_err(as_f64(to_np(got, dt), dt), ref) <= TOL_AFFINE
