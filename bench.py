@@ -365,11 +365,14 @@ def bench_llama_decode(ops, Ms=(1, 4, 8, 16, 32), steps=5):
     return out
 
 
-def _graph_layers(fns, reps=5):
-    """Average device time of one pass over fns (captured once as a graph)."""
+def _graph_layers(fns, reps=5, inner=1):
+    """Average device time of one pass over fns: `inner` passes are captured in
+    one graph (so the graph's own launch cost, ~10 us, is spread over them)
+    and the graph is replayed `reps` times."""
     def step():
-        for f in fns:
-            f()
+        for _ in range(inner):
+            for f in fns:
+                f()
     step()
     _warm_on_capture_stream(step)
     torch.cuda.synchronize()
@@ -386,7 +389,7 @@ def _graph_layers(fns, reps=5):
     t1.record()
     torch.cuda.synchronize()
     del g
-    return t0.elapsed_time(t1) * 1e-3 / reps
+    return t0.elapsed_time(t1) * 1e-3 / (reps * inner)
 
 
 def bench_fused(ops, Ms=(1, 4, 16), layers=32):
@@ -472,12 +475,12 @@ def bench_fused(ops, Ms=(1, 4, 16), layers=32):
             o.index_add_(0, order // k, y.float() * sc.reshape(-1)[order].unsqueeze(-1))
             return o
 
-        td = _graph_layers([on_device], reps=10)
-        tt = _graph_layers([torch_routing], reps=10)
+        td = _graph_layers([on_device], reps=10, inner=16 if T == 1 else 4)
+        tt = _graph_layers([torch_routing], reps=10, inner=16 if T == 1 else 4)
         moe[str(T)] = {"device_routing_fused_us": round(td * 1e6, 2), "torch_routing_split_us": round(tt * 1e6, 2)}
         if T == 1:
             # route + experts + combine of one token in two launches (ops.moe_token)
-            tk = _graph_layers([lambda: dev.token_forward(x, logits)], reps=10)
+            tk = _graph_layers([lambda: dev.token_forward(x, logits)], reps=10, inner=16)
             moe[str(T)]["one_token_kernels_us"] = round(tk * 1e6, 2)
     out["qwen_moe_expert_block"] = moe
     del gu_w, down_w, fused_ex, split_ex
@@ -488,7 +491,7 @@ def bench_fused(ops, Ms=(1, 4, 16), layers=32):
     emb = {}
     for T in (1, 512):
         tok = torch.randint(0, V, (T,), generator=gen, device="cuda")
-        tg = _graph_layers([lambda: ops.dequantize_rows(ew, es, eb, tok, 64, 4)], reps=10)
+        tg = _graph_layers([lambda: ops.dequantize_rows(ew, es, eb, tok, 64, 4)], reps=10, inner=16)
         tf = _graph_layers([lambda: ops.dequantize(ew, es, eb, 64, 4).index_select(0, tok)], reps=3)
         emb[str(T)] = {"row_gather_us": round(tg * 1e6, 2), "full_table_dequant_us": round(tf * 1e6, 2)}
     # dequantize alone: packed codes + scales / biases in, bf16 out

@@ -96,6 +96,73 @@ __global__ __launch_bounds__(256) void dequant_kernel(ConvArgs a, int64_t nchunk
   }
 }
 
+// Row-segment dequantize for affine 2-, 4- and 8-bit codes into 16-bit
+// outputs.  Block b takes segment b % segs of output row b / segs; thread t
+// takes packed words w0 + t + 256 u (U per thread, all loads issued before any
+// arithmetic), and writes each word's 32 / BITS values as one contiguous 8-,
+// 16- or 32-byte store, so a wave's store instruction covers one contiguous
+// span (dequant_kernel's one-chunk-per-thread layout writes 64-byte pieces
+// 16 bytes at a time).  Same arithmetic as dequant_kernel: s * q (exact in
+// fp32) + b, rounded once to the output type.
+template <int SDT, int ODT, int BITS, int U>
+__global__ __launch_bounds__(256) void dequant_words_kernel(ConvArgs a, int segs) {
+  using SS = typename Store<SDT>::T;
+  constexpr int CPW = 32 / BITS;  // codes per word
+  const int K = a.K, W = K / CPW, G = K / a.gs;
+  const int gshift = __builtin_ctz(a.gs);
+  const int64_t orow = blockIdx.x / segs;
+  const int w0 = static_cast<int>(blockIdx.x - orow * segs) * 256 * U + static_cast<int>(threadIdx.x);
+  uint16_t* dst = static_cast<uint16_t*>(a.out) + orow * K;
+  int64_t row = orow;
+  if (a.idx != nullptr) {
+    row = load_index(a.idx, a.idx_dt, orow);
+    if (row < 0) row += a.table_rows;
+    if (row < 0 || row >= a.table_rows) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int wi = w0 + 256 * u;
+        if (wi < W)
+          for (int j = 0; j < CPW; ++j) dst[wi * CPW + j] = from_f<ODT>(__builtin_nanf(""));
+      }
+      return;
+    }
+  }
+  const uint32_t* src = a.w + row * W;
+  const SS* sp = static_cast<const SS*>(a.s) + row * G;
+  const SS* bp = static_cast<const SS*>(a.b) + row * G;
+  uint32_t wd[U];
+  SS sv[U], bv[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int wi = min(w0 + 256 * u, W - 1);
+    wd[u] = __builtin_nontemporal_load(src + wi);
+    sv[u] = sp[(wi * CPW) >> gshift];
+    bv[u] = bp[(wi * CPW) >> gshift];
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int wi = w0 + 256 * u;
+    if (wi >= W) break;
+    const float s0 = to_f<SDT>(sv[u]), b0 = to_f<SDT>(bv[u]);
+    uint32_t o[CPW / 2];
+#pragma unroll
+    for (int j = 0; j < CPW / 2; ++j) {
+      const uint32_t q0 = (wd[u] >> (2 * j * BITS)) & ((1u << BITS) - 1);
+      const uint32_t q1 = (wd[u] >> ((2 * j + 1) * BITS)) & ((1u << BITS) - 1);
+      const float p0 = s0 * static_cast<float>(q0), p1 = s0 * static_cast<float>(q1);
+      o[j] = static_cast<uint32_t>(from_f<ODT>(p0 + b0)) | (static_cast<uint32_t>(from_f<ODT>(p1 + b0)) << 16);
+    }
+    uint16_t* d = dst + wi * CPW;
+    if constexpr (BITS == 8) {
+      *reinterpret_cast<uint2*>(d) = make_uint2(o[0], o[1]);
+    } else {
+#pragma unroll
+      for (int h = 0; h < CPW / 8; ++h)
+        reinterpret_cast<uint4*>(d)[h] = make_uint4(o[4 * h], o[4 * h + 1], o[4 * h + 2], o[4 * h + 3]);
+    }
+  }
+}
+
 // round-to-nearest-even onto the element grid with saturation, written as the
 // same grid search as the CPU restatement so ties and zero signs agree
 template <int MODE>
@@ -261,9 +328,33 @@ hipError_t quant_by_mode(const ConvArgs& a, int64_t ngroups, dim3 grid) {
 }
 }  // namespace
 
+template <int SDT, int ODT>
+hipError_t deq_words(const ConvArgs& a) {
+  const int W = a.K * a.bits / 32;
+  constexpr int U = 2;
+  const int segs = (W + 256 * U - 1) / (256 * U);
+  const int64_t nblk = a.rows * segs;
+  if (nblk > 0x7fffffffLL) return hipErrorInvalidConfiguration;
+  const dim3 grid(static_cast<unsigned>(nblk));
+  switch (a.bits) {
+    case 2: hipLaunchKernelGGL((dequant_words_kernel<SDT, ODT, 2, U>), grid, dim3(256), 0, a.stream, a, segs); break;
+    case 4: hipLaunchKernelGGL((dequant_words_kernel<SDT, ODT, 4, U>), grid, dim3(256), 0, a.stream, a, segs); break;
+    default: hipLaunchKernelGGL((dequant_words_kernel<SDT, ODT, 8, U>), grid, dim3(256), 0, a.stream, a, segs); break;
+  }
+  return hipGetLastError();
+}
+
 hipError_t launch_dequantize(const ConvArgs& a) {
   const int64_t nchunks = a.rows * ((a.K + 31) / 32);
   if (nchunks == 0) return hipSuccess;
+  // affine 2 / 4 / 8-bit into bf16 / fp16 (K a multiple of the group size,
+  // itself a multiple of 32): the row-segment kernel (128256 x 4096 q4 table:
+  // 364 -> 237 us, 3.7 -> 5.7 TB/s)
+  if (a.mode == AFFINE && (a.bits == 2 || a.bits == 4 || a.bits == 8) && (a.odt == F16 || a.odt == BF16) &&
+      a.K % a.gs == 0 && a.K % 32 == 0 && a.sdt != F32) {
+    if (a.odt == BF16) return a.sdt == BF16 ? deq_words<BF16, BF16>(a) : deq_words<F16, BF16>(a);
+    return a.sdt == BF16 ? deq_words<BF16, F16>(a) : deq_words<F16, F16>(a);
+  }
   const int64_t nblk = (nchunks + 255) / 256;
   if (nblk > 0x7fffffffLL) return hipErrorInvalidConfiguration;
   dim3 grid(static_cast<unsigned>(nblk));

@@ -51,6 +51,19 @@ def test_dequantize_affine_bit_exact(ops, bits, gs, sdt):
     _bits_equal(got, ref, sdt)
 
 
+@pytest.mark.parametrize("bits", [2, 4, 8])
+@pytest.mark.parametrize("K,sdt", [(16384, "bf16"), (4160, "f16")])
+def test_dequantize_long_rows_bit_exact(ops, bits, K, sdt):
+    """Rows of several 512-word segments (and a partial last one): the
+    row-segment kernel's multi-block rows."""
+    rng = np.random.default_rng(300 + bits + K % 7)
+    w, s, b = rand_affine(rng, 5, K, 64 if K % 64 == 0 else 32, bits, sdt)
+    gs = 64 if K % 64 == 0 else 32
+    got = ops.dequantize(words_to_torch(w), from_np(s, sdt), from_np(b, sdt), gs, bits)
+    ref = oracle.dequantize(w, s, b, sdt, gs, bits)
+    _bits_equal(got, ref, sdt)
+
+
 @pytest.mark.parametrize("odt", ["f32", "f16", "bf16"])
 @pytest.mark.parametrize("mode", ["mxfp4", "mxfp8", "nvfp4"])
 def test_dequantize_fp_bit_exact(ops, mode, odt):
