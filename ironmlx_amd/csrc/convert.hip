@@ -96,23 +96,28 @@ __global__ __launch_bounds__(256) void dequant_kernel(ConvArgs a, int64_t nchunk
   }
 }
 
-// Row-segment dequantize for affine 2-, 4- and 8-bit codes into 16-bit
-// outputs.  Block b takes segment b % segs of output row b / segs; thread t
+// Row-segment dequantize (affine 2-, 4- and 8-bit codes; mxfp4, nvfp4,
+// mxfp8).  Block b takes segment b % segs of output row b / segs; thread t
 // takes packed words w0 + t + 256 u (U per thread, all loads issued before any
-// arithmetic), and writes each word's 32 / BITS values as one contiguous 8-,
-// 16- or 32-byte store, so a wave's store instruction covers one contiguous
-// span (dequant_kernel's one-chunk-per-thread layout writes 64-byte pieces
-// 16 bytes at a time).  Same arithmetic as dequant_kernel: s * q (exact in
-// fp32) + b, rounded once to the output type.
-template <int SDT, int ODT, int BITS, int U>
+// arithmetic) and writes each word's 32 / BITS values as one contiguous
+// store of 8 to 64 bytes, so a wave's store instruction covers one contiguous
+// span (dequant_kernel's one-chunk-per-thread layout writes each thread's
+// piece 16 bytes at a time, 64 bytes apart across lanes).  A word's codes lie
+// in one group (groups are 16 codes or more).  Same arithmetic as
+// dequant_kernel: s * q (exact in fp32) + b, or the fp element times its
+// scale, rounded once to the output type.
+template <int SDT, int ODT, int MODE, int BITS, int U>
 __global__ __launch_bounds__(256) void dequant_words_kernel(ConvArgs a, int segs) {
-  using SS = typename Store<SDT>::T;
+  constexpr bool AFF = MODE == AFFINE;
+  using SS = typename Store<AFF ? SDT : U8>::T;
+  using OS = typename Store<ODT>::T;
   constexpr int CPW = 32 / BITS;  // codes per word
-  const int K = a.K, W = K / CPW, G = K / a.gs;
-  const int gshift = __builtin_ctz(a.gs);
+  const int gs = AFF ? a.gs : ModeInfo<MODE>::GS;
+  const int K = a.K, W = K / CPW, G = K / gs;
+  const int gshift = __builtin_ctz(gs);
   const int64_t orow = blockIdx.x / segs;
   const int w0 = static_cast<int>(blockIdx.x - orow * segs) * 256 * U + static_cast<int>(threadIdx.x);
-  uint16_t* dst = static_cast<uint16_t*>(a.out) + orow * K;
+  OS* dst = static_cast<OS*>(a.out) + orow * K;
   int64_t row = orow;
   if (a.idx != nullptr) {
     row = load_index(a.idx, a.idx_dt, orow);
@@ -129,7 +134,7 @@ __global__ __launch_bounds__(256) void dequant_words_kernel(ConvArgs a, int segs
   }
   const uint32_t* src = a.w + row * W;
   const SS* sp = static_cast<const SS*>(a.s) + row * G;
-  const SS* bp = static_cast<const SS*>(a.b) + row * G;
+  const SS* bp = AFF ? static_cast<const SS*>(a.b) + row * G : nullptr;
   uint32_t wd[U];
   SS sv[U], bv[U];
 #pragma unroll
@@ -137,27 +142,45 @@ __global__ __launch_bounds__(256) void dequant_words_kernel(ConvArgs a, int segs
     const int wi = min(w0 + 256 * u, W - 1);
     wd[u] = __builtin_nontemporal_load(src + wi);
     sv[u] = sp[(wi * CPW) >> gshift];
-    bv[u] = bp[(wi * CPW) >> gshift];
+    if constexpr (AFF) bv[u] = bp[(wi * CPW) >> gshift];
   }
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const int wi = w0 + 256 * u;
     if (wi >= W) break;
-    const float s0 = to_f<SDT>(sv[u]), b0 = to_f<SDT>(bv[u]);
-    uint32_t o[CPW / 2];
-#pragma unroll
-    for (int j = 0; j < CPW / 2; ++j) {
-      const uint32_t q0 = (wd[u] >> (2 * j * BITS)) & ((1u << BITS) - 1);
-      const uint32_t q1 = (wd[u] >> ((2 * j + 1) * BITS)) & ((1u << BITS) - 1);
-      const float p0 = s0 * static_cast<float>(q0), p1 = s0 * static_cast<float>(q1);
-      o[j] = static_cast<uint32_t>(from_f<ODT>(p0 + b0)) | (static_cast<uint32_t>(from_f<ODT>(p1 + b0)) << 16);
+    float s0, b0 = 0.f;
+    if constexpr (AFF) {
+      s0 = to_f<SDT>(sv[u]);
+      b0 = to_f<SDT>(bv[u]);
+    } else {
+      s0 = fp_scale<MODE>(sv[u]);
     }
-    uint16_t* d = dst + wi * CPW;
-    if constexpr (BITS == 8) {
+    uint32_t o[CPW * sizeof(OS) / 4];
+#pragma unroll
+    for (int j = 0; j < CPW; ++j) {
+      const uint32_t q = (wd[u] >> (j * BITS)) & ((1u << BITS) - 1);
+      float v;
+      if constexpr (AFF) {
+        const float p = s0 * static_cast<float>(q);
+        v = p + b0;
+      } else {
+        v = fp_elem<MODE>(q) * s0;
+      }
+      const OS e = from_f<ODT>(v);
+      if constexpr (sizeof(OS) == 4) {
+        o[j] = __builtin_bit_cast(uint32_t, e);
+      } else {
+        if (j % 2 == 0) o[j / 2] = static_cast<uint32_t>(e);
+        else o[j / 2] |= static_cast<uint32_t>(e) << 16;
+      }
+    }
+    OS* d = dst + wi * CPW;
+    constexpr int NB = CPW * static_cast<int>(sizeof(OS));  // bytes per word's values
+    if constexpr (NB == 8) {
       *reinterpret_cast<uint2*>(d) = make_uint2(o[0], o[1]);
     } else {
 #pragma unroll
-      for (int h = 0; h < CPW / 8; ++h)
+      for (int h = 0; h < NB / 16; ++h)
         reinterpret_cast<uint4*>(d)[h] = make_uint4(o[4 * h], o[4 * h + 1], o[4 * h + 2], o[4 * h + 3]);
     }
   }
@@ -328,32 +351,57 @@ hipError_t quant_by_mode(const ConvArgs& a, int64_t ngroups, dim3 grid) {
 }
 }  // namespace
 
-template <int SDT, int ODT>
-hipError_t deq_words(const ConvArgs& a) {
-  const int W = a.K * a.bits / 32;
+template <int SDT, int ODT, int MODE, int BITS>
+hipError_t deq_words_go(const ConvArgs& a) {
   constexpr int U = 2;
+  const int W = a.K * BITS / 32;
   const int segs = (W + 256 * U - 1) / (256 * U);
   const int64_t nblk = a.rows * segs;
   if (nblk > 0x7fffffffLL) return hipErrorInvalidConfiguration;
-  const dim3 grid(static_cast<unsigned>(nblk));
-  switch (a.bits) {
-    case 2: hipLaunchKernelGGL((dequant_words_kernel<SDT, ODT, 2, U>), grid, dim3(256), 0, a.stream, a, segs); break;
-    case 4: hipLaunchKernelGGL((dequant_words_kernel<SDT, ODT, 4, U>), grid, dim3(256), 0, a.stream, a, segs); break;
-    default: hipLaunchKernelGGL((dequant_words_kernel<SDT, ODT, 8, U>), grid, dim3(256), 0, a.stream, a, segs); break;
-  }
+  hipLaunchKernelGGL((dequant_words_kernel<SDT, ODT, MODE, BITS, U>), dim3(static_cast<unsigned>(nblk)), dim3(256), 0,
+                     a.stream, a, segs);
   return hipGetLastError();
+}
+
+template <int SDT, int ODT>
+hipError_t deq_words(const ConvArgs& a) {
+  switch (a.mode) {
+    case MXFP4: return deq_words_go<U8, ODT, MXFP4, 4>(a);
+    case NVFP4: return deq_words_go<U8, ODT, NVFP4, 4>(a);
+    case MXFP8: return deq_words_go<U8, ODT, MXFP8, 8>(a);
+  }
+  switch (a.bits) {
+    case 2: return deq_words_go<SDT, ODT, AFFINE, 2>(a);
+    case 4: return deq_words_go<SDT, ODT, AFFINE, 4>(a);
+    default: return deq_words_go<SDT, ODT, AFFINE, 8>(a);
+  }
+}
+
+template <int ODT>
+hipError_t deq_words_sdt(const ConvArgs& a) {
+  if (a.mode != AFFINE) return deq_words<U8, ODT>(a);
+  switch (a.sdt) {
+    case F32: return deq_words<F32, ODT>(a);
+    case F16: return deq_words<F16, ODT>(a);
+    default: return deq_words<BF16, ODT>(a);
+  }
 }
 
 hipError_t launch_dequantize(const ConvArgs& a) {
   const int64_t nchunks = a.rows * ((a.K + 31) / 32);
   if (nchunks == 0) return hipSuccess;
-  // affine 2 / 4 / 8-bit into bf16 / fp16 (K a multiple of the group size,
-  // itself a multiple of 32): the row-segment kernel (128256 x 4096 q4 table:
-  // 364 -> 237 us, 3.7 -> 5.7 TB/s)
-  if (a.mode == AFFINE && (a.bits == 2 || a.bits == 4 || a.bits == 8) && (a.odt == F16 || a.odt == BF16) &&
-      a.K % a.gs == 0 && a.K % 32 == 0 && a.sdt != F32) {
-    if (a.odt == BF16) return a.sdt == BF16 ? deq_words<BF16, BF16>(a) : deq_words<F16, BF16>(a);
-    return a.sdt == BF16 ? deq_words<BF16, F16>(a) : deq_words<F16, F16>(a);
+  // whole words of one group each (affine 2 / 4 / 8-bit, the fp modes): the
+  // row-segment kernel (128256 x 4096 q4 table into bf16: 364 -> 237 us,
+  // 3.7 -> 5.7 TB/s); 3 / 5 / 6-bit codes keep the chunk kernel
+  const bool words = a.mode != AFFINE || a.bits == 2 || a.bits == 4 || a.bits == 8;
+  const int gsz = a.mode == AFFINE ? a.gs : a.mode == NVFP4 ? 16 : 32;
+  if (words && a.K % gsz == 0 && a.K % 32 == 0) {
+    switch (a.odt) {
+      case F32: return deq_words_sdt<F32>(a);
+      case F16: return deq_words_sdt<F16>(a);
+      case BF16: return deq_words_sdt<BF16>(a);
+    }
+    return hipErrorInvalidValue;
   }
   const int64_t nblk = (nchunks + 255) / 256;
   if (nblk > 0x7fffffffLL) return hipErrorInvalidConfiguration;
