@@ -508,9 +508,14 @@ template <int XT, int CPL>
 hipError_t launch_ord_cpl(const QmmArgs& a) {
   // rows per wave (measured on MI355X): 2 from 4096 rows, 4 from 24576 rows
   // (x and the per-chunk setup amortize over more rows once the grid is
-  // large), 1 below 4096 rows so small matrices still spread over the CUs
+  // large), 1 below 4096 rows so small matrices still spread over the CUs.
+  // One plain matrix at M = 1 whose two-row waves share x through LDS (from
+  // 10240 rows, launch_ord) keeps two rows up to 65536 rows (N = 28672:
+  // 14.1 -> 13.1-13.7 us).
   const int64_t rows = static_cast<int64_t>(a.glu ? 2 * a.N : a.N) * a.nbatch;
-  int rb = rows >= 24576 ? 4 : rows >= 4096 ? 2 : 1;
+  const bool mapped = a.bm.ndim != 0 || a.bm.lhs != nullptr || a.bm.rhs != nullptr;
+  const bool shared_x = CPL == 2 && !a.glu && a.M == 1 && a.nbatch == 1 && !mapped && a.mode == AFFINE;
+  int rb = rows >= (shared_x ? 65536 : 24576) ? 4 : rows >= 4096 ? 2 : 1;
   if (CPL >= 4 && rb > 2) rb = 2;
   if (a.glu && rb < 2) rb = 2;  // a gate row and its up row per output
   switch (rb) {

@@ -231,7 +231,8 @@ def test_streaming_decode_widths_vs_oracle(ops, N, M, gs, dt):
     assert rel_err(as_f64(to_np(got, dt), dt), ref) <= TOL_AFFINE
 
 
-@pytest.mark.parametrize("N,K,dt", [(10250, 4096, "f16"), (20482, 4096, "bf16"), (12000, 3072, "bf16")])
+@pytest.mark.parametrize("N,K,dt", [(10250, 4096, "f16"), (20482, 4096, "bf16"), (12000, 3072, "bf16"),
+                                    (28672, 4096, "bf16")])
 def test_shared_x_gemv_vs_oracle(ops, N, K, dt):
     """The one-row GEMV with four waves sharing x through LDS (from 10240
     rows): a ragged last workgroup (rows past N) and a K that leaves some
