@@ -486,10 +486,11 @@ hipError_t launch_ord(const QmmArgs& a) {
     }
     if (a.mode == MXFP4) { launch_mr<XT, RB, CPL, 1, MXFP4, false, KS>(grid, a, p, mapped, b0); continue; }
     if (a.mode == NVFP4) { launch_mr<XT, RB, CPL, 1, NVFP4, false, KS>(grid, a, p, mapped, b0); continue; }
-    // four waves sharing x through LDS (measured, K = 4096, two rows per
-    // wave: N = 11008 / 14336 / 20480: 7.5 / 8.9 / 11.8 -> 7.2 / 8.3 / 10.5 us;
-    // even at 8192 rows, behind at 6144 and for the SwiGLU rows)
-    if constexpr (KS == 1 && RB == 2 && CPL == 2) {
+    // four waves sharing x through LDS (measured, two rows per wave: K = 4096,
+    // N = 11008 / 14336 / 20480: 7.5 / 8.9 / 11.8 -> 7.2 / 8.3 / 10.5 us;
+    // K = 2048 / 6144 / 8192: 3-9% faster; even at 8192 rows, behind at 6144
+    // and for the SwiGLU rows)
+    if constexpr (KS == 1 && RB == 2) {
       if (a.M == 1 && !mapped && a.N >= 10240) {
         launch_mr<XT, RB, CPL, 1, AFFINE, false, KS, 4>(grid, a, p, mapped, b0);
         continue;
@@ -514,7 +515,7 @@ hipError_t launch_ord_cpl(const QmmArgs& a) {
   // 14.1 -> 13.1-13.7 us).
   const int64_t rows = static_cast<int64_t>(a.glu ? 2 * a.N : a.N) * a.nbatch;
   const bool mapped = a.bm.ndim != 0 || a.bm.lhs != nullptr || a.bm.rhs != nullptr;
-  const bool shared_x = CPL == 2 && !a.glu && a.M == 1 && a.nbatch == 1 && !mapped && a.mode == AFFINE;
+  const bool shared_x = !a.glu && a.M == 1 && a.nbatch == 1 && !mapped && a.mode == AFFINE;
   int rb = rows >= (shared_x ? 65536 : 24576) ? 4 : rows >= 4096 ? 2 : 1;
   if (CPL >= 4 && rb > 2) rb = 2;
   if (a.glu && rb < 2) rb = 2;  // a gate row and its up row per output

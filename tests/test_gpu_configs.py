@@ -232,7 +232,7 @@ def test_streaming_decode_widths_vs_oracle(ops, N, M, gs, dt):
 
 
 @pytest.mark.parametrize("N,K,dt", [(10250, 4096, "f16"), (20482, 4096, "bf16"), (12000, 3072, "bf16"),
-                                    (28672, 4096, "bf16")])
+                                    (28672, 4096, "bf16"), (16384, 2048, "bf16"), (10240, 8192, "f16")])
 def test_shared_x_gemv_vs_oracle(ops, N, K, dt):
     """The one-row GEMV with four waves sharing x through LDS (from 10240
     rows): a ragged last workgroup (rows past N) and a K that leaves some
