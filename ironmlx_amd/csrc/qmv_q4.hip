@@ -479,6 +479,14 @@ hipError_t launch_ord(const QmmArgs& a) {
     const int64_t nb = a.nbatch - b0 < 65535 ? a.nbatch - b0 : 65535;
     const dim3 grid(static_cast<unsigned>(nrb), static_cast<unsigned>(nb));
     if (a.glu) {
+      // gate / up row pairs sharing x the same way from 10240 rows (2 I =
+      // 12288: 8.6 -> 8.2 us; even at 28672 rows, which keep four rows per wave)
+      if constexpr (KS == 1 && RB == 2) {
+        if (a.mode == AFFINE && !mapped && 2 * static_cast<int64_t>(a.N) >= 10240) {
+          launch_mr<XT, RB, CPL, 1, AFFINE, true, KS, 4>(grid, a, p, mapped, b0);
+          continue;
+        }
+      }
       if (a.mode == MXFP4) launch_mr<XT, RB, CPL, 1, MXFP4, true, KS>(grid, a, p, mapped, b0);
       else if (a.mode == NVFP4) launch_mr<XT, RB, CPL, 1, NVFP4, true, KS>(grid, a, p, mapped, b0);
       else launch_mr<XT, RB, CPL, 1, AFFINE, true, KS>(grid, a, p, mapped, b0);
@@ -489,7 +497,7 @@ hipError_t launch_ord(const QmmArgs& a) {
     // four waves sharing x through LDS (measured, two rows per wave: K = 4096,
     // N = 11008 / 14336 / 20480: 7.5 / 8.9 / 11.8 -> 7.2 / 8.3 / 10.5 us;
     // K = 2048 / 6144 / 8192: 3-9% faster; even at 8192 rows, behind at 6144
-    // and for the SwiGLU rows)
+    // for the SwiGLU rows at four rows per wave)
     if constexpr (KS == 1 && RB == 2) {
       if (a.M == 1 && !mapped && a.N >= 10240) {
         launch_mr<XT, RB, CPL, 1, AFFINE, false, KS, 4>(grid, a, p, mapped, b0);

@@ -245,3 +245,19 @@ def test_shared_x_gemv_vs_oracle(ops, N, K, dt):
     ref = oracle.qmv_affine(to_np(x, dt), dt, _words(wq), to_np(s, dt), to_np(b, dt), dt, 64, 4,
                             odt="f32", nthreads=NT)
     assert rel_err(as_f64(to_np(got, dt), dt), ref) <= TOL_AFFINE
+
+
+@pytest.mark.parametrize("I,dt", [(6144, "bf16"), (5203, "f16")])
+def test_shared_x_swiglu_rows_vs_oracle(ops, I, dt):
+    """The M = 1 fused SwiGLU with four gate / up wave pairs sharing x
+    (10240 <= 2I < 24576 rows), including a ragged last workgroup."""
+    K = 4096
+    tdt = torch.bfloat16 if dt == "bf16" else torch.float16
+    print(f"shared-x SwiGLU I={I} {dt}", flush=True)
+    wq, s, b = _weight(ops, 2 * I, K, seed=31 + I % 13, gs=64, dt=tdt)
+    x = _x(1, K, seed=90, dt=tdt)
+    got = ops.quantized_swiglu(x, wq, s, b, 64, 4)
+    gu = oracle.qmv_affine(to_np(x, dt), dt, _words(wq), to_np(s, dt), to_np(b, dt), dt, 64, 4,
+                           odt=dt, nthreads=NT)
+    ref = as_f64(oracle.swiglu(gu, dt), dt)
+    assert rel_err(as_f64(to_np(got, dt), dt), ref) <= TOL_AFFINE
