@@ -1087,6 +1087,7 @@ hipError_t gemm_launch_t(const QmmArgs& a) {
     const bool one_w = a.bm.ndim == 0 && a.bm.lhs == nullptr && a.bm.rhs == nullptr;
     if (dma_ok && one_w && a.K % (32 * (OB == 4 ? 4 : 2)) == 0 && G % GPC == 0) {
       const int64_t nchunks = static_cast<int64_t>(a.N) * (a.K / 32);
+      if ((nchunks + 255) / 256 > 0x7fffffffLL) return hipErrorInvalidConfiguration;
       void* ws = nullptr;
       hipError_t e = workspace_get(a.stream, WS_CODES, static_cast<size_t>(nchunks) * OB * 4, &ws);
       if (e != hipSuccess) return e;
