@@ -130,4 +130,24 @@ __device__ __forceinline__ void fac_block(f32x4d_t (&Y)[NT][MT], const g_u32x4_t
   fac_block_xs<XT, NT, MT, GB, SW>(Y, A, XG, wst, h, hb, sw, bw, r, q);
 }
 
+// LDS plan of the streaming kernels (qmm_stream.hip, qmm_gather.hip): per
+// wave a ring of D weight stages plus double-buffered scale / bias words, and
+// the cross-wave partial sums of one tile-block.
+template <int NT, int MT, int S, int D, int SW>
+struct StreamLds {
+  static constexpr int WST = NT * 2048;           // one stage of a wave's weights: NT*16 rows x 128 B
+  static constexpr int SCL = NT * 16 * SW * 4;    // a tile-block's scale (or bias) words, one wave
+  static constexpr int WAVE = D * WST + 4 * SCL;  // ring + double-buffered scales and biases
+  static constexpr int RED = S * NT * MT * 1024;  // cross-wave partial sums of one tile-block
+  static constexpr int TOTAL = S * WAVE + RED;
+};
+
+template <int NT, int MT, int S, int D, int KB, int GB>
+constexpr bool stream_fits() {
+  constexpr int SW = KB * GB / 2;
+  constexpr int NDW = 2 * NT, NSC = (2 * NT * 16 * (SW / 4) + 63) / 64;
+  return KB % 2 == 0 && SW % 4 == 0 && D >= 2 && D <= 3 && StreamLds<NT, MT, S, D, SW>::TOTAL <= 160 * 1024 &&
+         (D - 2) * (2 * NDW + NSC) < 64;
+}
+
 }  // namespace iqmm

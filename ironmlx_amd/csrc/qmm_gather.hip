@@ -1,5 +1,6 @@
 // qmm_gather.hip — sorted grouped gather_qmm (affine 4-bit, gs 32 / 64 / 128)
 // with the factored MFMA arithmetic of qmm_decode.hip.
+#include <algorithm>
 #include <type_traits>
 
 #include "launch.h"
@@ -267,6 +268,201 @@ __global__ __launch_bounds__(64 * S) void gather_decode_kernel(QmmArgs a, int64_
   }
 }
 
+// Sorted grouped gather_qmm streamed per expert (the MoE layer of
+// mlx/src/nn/moe.rs:84-170 over mlx/src/model/qwen35.rs:653-775's stacked
+// experts): workgroup (expert e, part z of Z) takes tile-blocks z, z + Z, ...
+// of expert e's N weight rows for each 16-row pass over the expert's rows.
+// Per pass, each of its S waves loads the x operands of its K range (KB
+// 128-code blocks) for the pass's rows ONCE -- gathered through the row
+// table, held in registers with their group sums -- and then streams its
+// tile-blocks (one 16-row weight tile, or a gate tile with its up tile for the
+// SwiGLU) through a D-stage LDS ring by LDS DMA, as qmm_stream_kernel does; the
+// S partial sums of each tile-block meet in LDS and the workgroup stores the
+// pass's rows.  Against gather_decode_kernel (one 64-column block per
+// workgroup), the x rows are fetched and converted once per pass instead of
+// once per column block.  Workgroups e = E write NaN for batch entries outside
+// every expert's segment; rows whose lhs index is out of range are NaN.
+template <int XT, int NT, int GB, int S, int D, int KB, bool GLU>
+__global__ __launch_bounds__(64 * S) void gather_stream_kernel(QmmArgs a, int64_t nflat, const int64_t* off, int Z) {
+  constexpr int MT = 1;
+  static_assert(!GLU || NT == 2, "GLU pairs one gate tile with its up tile");
+  static_assert(stream_fits<NT, MT, S, D, KB, GB>(), "LDS / vmcnt budget");
+  constexpr int NS = KB / 2;                  // stages per tile-block
+  constexpr int SW = KB * GB / 2;             // scale words per row in a wave's K range
+  using L = StreamLds<NT, MT, S, D, SW>;
+  constexpr int NDW = 2 * NT;                 // weight DMA per stage
+  constexpr int PSC = NT * 16 * (SW / 4);     // 16-byte scale pieces per tile-block (biases as many)
+  constexpr int NSC = (2 * PSC + 63) / 64;    // scale + bias DMA with the first stage
+  constexpr int NC = GLU ? 8 * NT : 16 * NT;  // output columns per tile-block
+  using XS = uint16_t;
+  __shared__ __attribute__((aligned(1024))) char lds[L::TOTAL];
+  __shared__ int64_t prow_x[16], prow_o[16];
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int Mx = a.M, N = a.N, K = a.K;
+  const int r = lane & 15, q = lane >> 4;
+  const int pb = KB * wave;
+  const int64_t e = blockIdx.x / Z;
+  const int z = static_cast<int>(blockIdx.x - e * Z);
+  XS* out = static_cast<XS*>(a.out);
+  if (e == a.bm.nw) {
+    if (z != 0) return;
+    // offsets are clamped into [0, nflat]: indices that are not sorted as
+    // promised give wrong rows, never out-of-range accesses
+    const int64_t first_valid = min(max(off[0], int64_t{0}), nflat);
+    const int64_t end_valid = min(max(off[e], first_valid), nflat);
+    const int64_t nbad = first_valid + (nflat - end_valid);
+    for (int64_t i = t; i < nbad * Mx * N; i += 64 * S) {
+      const int64_t rr = i / N, n = i % N;
+      const int64_t bi = rr / Mx, mrow = rr % Mx;
+      const int64_t b = bi < first_valid ? bi : end_valid + (bi - first_valid);
+      out[(b * Mx + mrow) * N + n] = from_f<XT>(__builtin_nanf(""));
+    }
+    return;
+  }
+  const int64_t blo = min(max(off[e], int64_t{0}), nflat);
+  const int64_t bhi = min(max(off[e + 1], blo), nflat);
+  if (blo >= bhi) return;  // workgroup-uniform
+  const int64_t rows_total = (bhi - blo) * Mx;
+  const int gshift = __builtin_ctz(a.gs);
+  const int64_t wrow = K / 2, srow = (K >> gshift) * 2;
+  const char* w = reinterpret_cast<const char*>(a.w + e * a.w_mat);
+  const char* sp = reinterpret_cast<const char*>(static_cast<const XS*>(a.s) + e * a.s_mat);
+  const char* bp = reinterpret_cast<const char*>(static_cast<const XS*>(a.b) + e * a.s_mat);
+  const XS* x = static_cast<const XS*>(a.x);
+  const int ntb = (N + NC - 1) / NC;
+  const int nit = z < ntb ? (ntb - z + Z - 1) / Z : 0;
+  if (nit == 0) return;  // workgroup-uniform
+  const int total = nit * NS;
+  auto wrow_of = [&](int tb, int row) {  // tile-block row -> weight row of the expert
+    const int tt = row >> 4, rr = row & 15, n0 = tb * NC;
+    return GLU ? static_cast<int64_t>(tt) * N + min(n0 + rr, N - 1) : static_cast<int64_t>(min(n0 + row, N - 1));
+  };
+  const uint32_t lds_wave = __builtin_amdgcn_readfirstlane(lds_u32(lds)) + wave * L::WAVE;
+  const char* lds_w = lds + wave * L::WAVE;
+  float* red = reinterpret_cast<float*>(lds + S * L::WAVE);
+  auto issue = [&](int it, int st) {
+    const int tb = z + Z * it;
+    const int slot = (it * NS + st) % D;
+#pragma unroll
+    for (int u = 0; u < NDW; ++u) {
+      const int row = 8 * u + (lane >> 3);
+      dma16(w + wrow_of(tb, row) * wrow + pb * 64 + st * 128 + 16 * ((lane & 7) ^ (row & 7)),
+            lds_wave + slot * L::WST + u * 1024);
+    }
+    if (st == 0) {
+      const uint32_t sbase = lds_wave + D * L::WST + (it & 1) * 2 * L::SCL;
+#pragma unroll
+      for (int v = 0; v < NSC; ++v) {
+        const int p = 64 * v + lane;
+        if (p < 2 * PSC) {
+          const int which = p >= PSC, pp = p - which * PSC;
+          const int row = pp / (SW / 4), part = pp % (SW / 4);
+          dma16((which ? bp : sp) + wrow_of(tb, row) * srow + pb * GB * 2 + part * 16, sbase + v * 1024);
+        }
+      }
+    }
+  };
+  for (int64_t r0 = 0; r0 < rows_total; r0 += 16) {
+    // row table of the pass: rows past the segment repeat its last row (their
+    // outputs are not stored)
+    if (t < 16) {
+      const int64_t rr = min(r0 + t, rows_total - 1);
+      const int64_t b = blo + rr / Mx, mrow = rr % Mx;
+      const int64_t xm = a.bm.lhs ? load_index(a.bm.lhs, a.bm.lhs_dt, b) : b;
+      const bool ok = xm >= 0 && xm < a.bm.nx;
+      prow_x[t] = (ok ? xm : 0) * a.x_mat + mrow * K;
+      prow_o[t] = ok ? (b * Mx + mrow) * N : ~((b * Mx + mrow) * N);
+    }
+    __syncthreads();
+    g_u32x4_t A[KB][MT][4];
+    {
+      const char* xr = reinterpret_cast<const char*>(x + prow_x[r]) + pb * 256 + 16 * q;
+#pragma unroll
+      for (int b = 0; b < KB; ++b)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) A[b][0][j] = x_pairs(*reinterpret_cast<const g_u32x4_t*>(xr + b * 256 + 64 * j));
+    }
+    // the compiler's own loads are complete before the counted DMA starts
+    __builtin_amdgcn_s_waitcnt(0);
+    constexpr bool PRE = MT * GB <= 2;
+    f32x4d_t XS_[PRE ? KB : 1][MT][GB];
+    if constexpr (PRE) {
+#pragma unroll
+      for (int b = 0; b < KB; ++b) block_xsums<XT, MT, GB>(XS_[b], A[b]);
+    }
+    f32x4d_t Y[NT][MT];
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) Y[tt][0] = f32x4d_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < D - 1; ++u)
+      if (u < total) issue(u / NS, u % NS);
+    uint32_t sw[NT][SW], bw[NT][SW];
+    for (int it = 0; it < nit; ++it) {
+#pragma unroll
+      for (int st = 0; st < NS; ++st) {
+        const int u = it * NS + st;
+        const int later = min(D - 2, total - 1 - u);
+        if (later >= 1) {
+          if ((st + 1) % NS == 0) vm_wait<(D >= 3 ? NDW + NSC : 0)>();
+          else vm_wait<(D >= 3 ? NDW : 0)>();
+        } else {
+          vm_wait<0>();
+        }
+        if (st == 0) {
+          const char* sb = lds_w + D * L::WST + (it & 1) * 2 * L::SCL;
+#pragma unroll
+          for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+            for (int h = 0; h < SW; ++h) {
+              sw[tt][h] = *reinterpret_cast<const uint32_t*>(sb + ((tt * 16 + r) * SW + h) * 4);
+              bw[tt][h] = *reinterpret_cast<const uint32_t*>(sb + L::SCL + ((tt * 16 + r) * SW + h) * 4);
+            }
+        }
+        if (u + D - 1 < total) {
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // slot (u - 1) % D has been read
+          issue((u + D - 1) / NS, (st + D - 1) % NS);
+        }
+        const char* wst = lds_w + (u % D) * L::WST;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          if constexpr (PRE)
+            fac_block_xs<XT, NT, MT, GB, SW>(Y, A[2 * st + h], XS_[2 * st + h], wst, h, (2 * st + h) * GB, sw, bw, r,
+                                             q);
+          else
+            fac_block<XT, NT, MT, GB, SW>(Y, A[2 * st + h], wst, h, (2 * st + h) * GB, sw, bw, r, q);
+        }
+      }
+      // the S partial sums of tile-block it meet in LDS
+      const int n0 = (z + Z * it) * NC;
+#pragma unroll
+      for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          red[(wave * NT + tt) * 256 + (4 * q + v) * 16 + r] = Y[tt][0][v];
+          Y[tt][0][v] = 0.f;
+        }
+      __syncthreads();
+      for (int idx = t; idx < 16 * NC; idx += 64 * S) {
+        const int m = idx / NC, nn = idx % NC;
+        if (r0 + m >= rows_total || n0 + nn >= N) continue;
+        float acc[2] = {0.f, 0.f};
+#pragma unroll
+        for (int hh = 0; hh < (GLU ? 2 : 1); ++hh) {
+          const int tt = GLU ? hh : (nn >> 4);
+#pragma unroll
+          for (int w2 = 0; w2 < S; ++w2) acc[hh] += red[(w2 * NT + tt) * 256 + m * 16 + (nn & 15)];
+        }
+        const int64_t o = prow_o[m];
+        const auto v = GLU ? swiglu_out<XT>(acc[0], acc[1]) : from_f<XT>(acc[0]);
+        if (o >= 0) out[o + n0 + nn] = v;
+        else out[~o + n0 + nn] = from_f<XT>(__builtin_nanf(""));
+      }
+      __syncthreads();  // the partials (and, after the last, the row table) are read before they are rewritten
+    }
+  }
+}
+
 struct GatCfg {
   int nt, s, d, kb;
   bool xl;
@@ -348,7 +544,66 @@ hipError_t gather_dec_gs(const QmmArgs& a, int64_t nflat, int64_t E, const int64
 }
 
 
+int gat_cu_count() {
+  static int n[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (n[dev] == 0) {
+    int c = 0;
+    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
+    n[dev] = c;
+  }
+  return n[dev];
+}
+
+template <int XT, int GB, bool GLU, int S>
+hipError_t gstream_go(const QmmArgs& a, int64_t nflat, int64_t E, const int64_t* off) {
+  constexpr int NT = GLU ? 2 : 1, D = 3, KB = 4;
+  if constexpr (!stream_fits<NT, 1, S, D, KB, GB>()) {
+    return hipErrorInvalidValue;
+  } else {
+    constexpr int NC = GLU ? 8 * NT : 16 * NT;
+    const int ntb = (a.N + NC - 1) / NC;
+    // about eight waves per CU over the experts: Z workgroups per expert
+    const int64_t want = (8LL * gat_cu_count() + E * S - 1) / (E * S);
+    const int Z = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(want, ntb)));
+    const int64_t nblk = (E + 1) * Z;
+    if (nblk > 0x7fffffffLL) return hipErrorInvalidConfiguration;
+    hipLaunchKernelGGL((gather_stream_kernel<XT, NT, GB, S, D, KB, GLU>), dim3(static_cast<unsigned>(nblk)),
+                       dim3(64 * S), 0, a.stream, a, nflat, off, Z);
+    return hipGetLastError();
+  }
+}
+
+template <int XT, int GB, bool GLU>
+hipError_t gstream_s(const QmmArgs& a, int64_t nflat, int64_t E, const int64_t* off) {
+  switch (a.K / 512) {
+    case 1: return gstream_go<XT, GB, GLU, 1>(a, nflat, E, off);
+    case 2: return gstream_go<XT, GB, GLU, 2>(a, nflat, E, off);
+    case 4: return gstream_go<XT, GB, GLU, 4>(a, nflat, E, off);
+    default: return gstream_go<XT, GB, GLU, 8>(a, nflat, E, off);
+  }
+}
+
+template <int XT>
+hipError_t gstream_xt(const QmmArgs& a, int64_t nflat, int64_t E, const int64_t* off) {
+  if (a.gs == 32) return a.glu ? gstream_s<XT, 4, true>(a, nflat, E, off) : gstream_s<XT, 4, false>(a, nflat, E, off);
+  return a.glu ? gstream_s<XT, 2, true>(a, nflat, E, off) : gstream_s<XT, 2, false>(a, nflat, E, off);
+}
+
 }  // namespace
+
+bool gather_stream_supported(const QmmArgs& a) {
+  return a.transpose && a.mode == AFFINE && a.bits == 4 && (a.xdt == BF16 || a.xdt == F16) &&
+         a.gs == 64 && a.bm.rhs != nullptr && a.N >= 1 &&
+         (a.K == 512 || a.K == 1024 || a.K == 2048 || a.K == 4096) && (a.K / a.gs) % 8 == 0 && a.b != nullptr &&
+         (reinterpret_cast<uintptr_t>(a.s) | reinterpret_cast<uintptr_t>(a.b)) % 16 == 0;
+}
+
+hipError_t launch_gather_stream(const QmmArgs& a, int64_t nflat, int64_t E, const int64_t* off) {
+  return a.xdt == BF16 ? gstream_xt<BF16>(a, nflat, E, off) : gstream_xt<F16>(a, nflat, E, off);
+}
+
 
 bool gather_decode_supported(const QmmArgs& a) {
   if (!(a.transpose && a.mode == AFFINE && a.bits == 4 && (a.xdt == BF16 || a.xdt == F16) && a.K % 128 == 0 &&

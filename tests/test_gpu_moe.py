@@ -151,6 +151,45 @@ def test_gather_qmm_swiglu_group_sizes(ops, gs, I, T):
     assert rel_err(as_f64(to_np(gu, dt).reshape(T * k, 2 * I), dt), refp) <= 1e-2
 
 
+@pytest.mark.parametrize("H,I,dt", [(2048, 512, "bf16"), (1024, 520, "f16"), (4096, 264, "bf16")])
+def test_gather_stream_few_rows_per_expert(ops, H, I, dt):
+    """Sorted gather_qmm with at most 8 rows per expert on average and K of
+    1024 or more: the per-expert streaming kernel (K = 1024 / 2048 / 4096:
+    two, four and eight waves; a ragged N; one lhs index out of range, whose
+    row is NaN).  The product against the oracle's per-row products, and the
+    fused SwiGLU bit-exact against the oracle's SwiGLU of that product."""
+    print(f"gather stream H={H} I={I} {dt}", flush=True)
+    rng = np.random.default_rng(H + I)
+    E, k, T = 64, 8, 40   # 320 rows over 64 experts: 5 per expert
+    wn, sn, bn = rand_affine(rng, 2 * I, H, 64, 4, dt, (E,))
+    w, s, b = words_to_torch(wn), from_np(sn, dt), from_np(bn, dt)
+    x = torch.randn(T, 1, H, generator=torch.Generator().manual_seed(H)).to(TDT[dt]).cuda()
+    ex = torch.from_numpy(np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32))
+    flat = ex.reshape(-1)
+    order = torch.argsort(flat, stable=True)
+    rhs = flat[order].contiguous().cuda()
+    lhs_h = (order // k).to(torch.int32)
+    lhs_h[7] = T + 3  # out of range: NaN row
+    lhs = lhs_h.contiguous().cuda()
+    gu = ops.gather_qmm(x, w, s, b, lhs, rhs, True, 64, 4, sorted_indices=True)
+    got = ops.gather_qmm_swiglu(x, w, s, b, lhs, rhs, 64, 4, sorted_indices=True)
+    torch.cuda.synchronize()
+    g = as_f64(to_np(gu, dt).reshape(T * k, 2 * I), dt)
+    assert np.all(np.isnan(g[7]))
+    ok = np.ones(T * k, bool)
+    ok[7] = False
+    xs = to_np(x[:, 0], dt)[np.clip(lhs_h.numpy(), 0, T - 1)]
+    rn = rhs.cpu().numpy()
+    refp = np.zeros((T * k, 2 * I))
+    for e in np.unique(rn):
+        rows = np.nonzero(rn == e)[0]
+        refp[rows] = oracle.qmv_affine(xs[rows], dt, wn[e], sn[e], bn[e], dt, 64, 4, odt="f32", nthreads=8)
+    assert rel_err(g[ok], refp[ok]) <= 1e-2
+    ref = oracle.swiglu(to_np(gu, dt).reshape(T * k, 2 * I)[ok], dt)
+    assert np.array_equal(_bits(got, dt).reshape(T * k, I)[ok], np.ascontiguousarray(ref).view(np.uint16))
+    assert np.all(np.isnan(as_f64(to_np(got, dt), dt).reshape(T * k, I)[7]))
+
+
 # ------------------------------------------------------------------ row gather
 @pytest.mark.parametrize("mode,bits,gs", [("affine", 4, 64), ("affine", 3, 32), ("affine", 8, 128),
                                           ("mxfp4", 4, 32), ("mxfp8", 8, 32), ("nvfp4", 4, 16)])
