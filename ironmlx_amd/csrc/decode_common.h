@@ -130,6 +130,35 @@ __device__ __forceinline__ void fac_block(f32x4d_t (&Y)[NT][MT], const g_u32x4_t
   fac_block_xs<XT, NT, MT, GB, SW>(Y, A, XG, wst, h, hb, sw, bw, r, q);
 }
 
+// Row segment of a sorted grouped gather found inside the kernel: the first
+// batch index i in [0, n] whose expert key is >= e, where the key is the rhs
+// index clamped into [-1, E] (the definition of segment_offsets_kernel's
+// off[e]).  A wave probes 64 evenly spaced entries per round and keeps the
+// interval where the sorted keys cross e: two dependent rounds for 4096
+// rows.  Every lane returns the same (wave-uniform) index; a rhs that is not
+// sorted as promised gives some index in [0, n], never an out-of-range one.
+__device__ __forceinline__ int64_t seg_lower_bound(const void* rhs, int dt, int64_t n, int64_t E, int64_t e,
+                                                   int lane) {
+  int64_t lo = 0, hi = n;
+  while (hi > lo) {
+    const int64_t len = hi - lo;
+    const int64_t step = (len + 63) / 64;
+    const int64_t p = lo + min(static_cast<int64_t>(lane) * step, len - 1);
+    int64_t v = load_index(rhs, dt, p);
+    v = v < 0 ? int64_t{-1} : v > E ? E : v;
+    const uint64_t m = __ballot(v >= e);
+    if (m == 0) {
+      lo = lo + min(63 * step, len - 1) + 1;  // every probe is below e
+    } else {
+      const int f = __builtin_ctzll(m);
+      const int64_t pf = lo + min(static_cast<int64_t>(f) * step, len - 1);
+      hi = pf;
+      if (f > 0) lo = lo + min(static_cast<int64_t>(f - 1) * step, len - 1) + 1;
+    }
+  }
+  return lo;
+}
+
 // LDS plan of the streaming kernels (qmm_stream.hip, qmm_gather.hip): per
 // wave a ring of D weight stages plus double-buffered scale / bias words, and
 // the cross-wave partial sums of one tile-block.

@@ -69,7 +69,7 @@ bool qmm_decode_supported(const QmmArgs& a);
 // grouped gather_qmm with the decode kernel's factored arithmetic (affine 4-bit)
 hipError_t launch_gather_decode(const QmmArgs& a, int64_t nflat, int64_t E, const int64_t* off);
 bool gather_decode_supported(const QmmArgs& a);
-hipError_t launch_gather_stream(const QmmArgs& a, int64_t nflat, int64_t E, const int64_t* off);
+hipError_t launch_gather_stream(const QmmArgs& a, int64_t nflat, int64_t E);  // finds its own row segments
 bool gather_stream_supported(const QmmArgs& a);
 // sorted-expert grouped gather_qmm: nflat batch elements, E experts
 hipError_t launch_gather_sorted(const QmmArgs& a, int64_t nflat, int64_t E);

@@ -280,10 +280,13 @@ __global__ __launch_bounds__(64 * S) void gather_decode_kernel(QmmArgs a, int64_
 // S partial sums of each tile-block meet in LDS and the workgroup stores the
 // pass's rows.  Against gather_decode_kernel (one 64-column block per
 // workgroup), the x rows are fetched and converted once per pass instead of
-// once per column block.  Workgroups e = E write NaN for batch entries outside
-// every expert's segment; rows whose lhs index is out of range are NaN.
+// once per column block.  Each workgroup finds its expert's row segment in the
+// sorted rhs itself (seg_lower_bound: two dependent probe rounds for 4096
+// rows), so no offsets pre-pass runs.  Workgroups e = E write NaN for batch
+// entries outside every expert's segment; rows whose lhs index is out of range
+// are NaN.
 template <int XT, int NT, int GB, int S, int D, int KB, bool GLU>
-__global__ __launch_bounds__(64 * S) void gather_stream_kernel(QmmArgs a, int64_t nflat, const int64_t* off, int Z) {
+__global__ __launch_bounds__(64 * S) void gather_stream_kernel(QmmArgs a, int64_t nflat, int Z) {
   constexpr int MT = 1;
   static_assert(!GLU || NT == 2, "GLU pairs one gate tile with its up tile");
   static_assert(stream_fits<NT, MT, S, D, KB, GB>(), "LDS / vmcnt budget");
@@ -309,8 +312,10 @@ __global__ __launch_bounds__(64 * S) void gather_stream_kernel(QmmArgs a, int64_
     if (z != 0) return;
     // offsets are clamped into [0, nflat]: indices that are not sorted as
     // promised give wrong rows, never out-of-range accesses
-    const int64_t first_valid = min(max(off[0], int64_t{0}), nflat);
-    const int64_t end_valid = min(max(off[e], first_valid), nflat);
+    const int64_t o0 = seg_lower_bound(a.bm.rhs, a.bm.rhs_dt, nflat, a.bm.nw, 0, lane);
+    const int64_t oE = seg_lower_bound(a.bm.rhs, a.bm.rhs_dt, nflat, a.bm.nw, e, lane);
+    const int64_t first_valid = min(max(o0, int64_t{0}), nflat);
+    const int64_t end_valid = min(max(oE, first_valid), nflat);
     const int64_t nbad = first_valid + (nflat - end_valid);
     for (int64_t i = t; i < nbad * Mx * N; i += 64 * S) {
       const int64_t rr = i / N, n = i % N;
@@ -320,8 +325,12 @@ __global__ __launch_bounds__(64 * S) void gather_stream_kernel(QmmArgs a, int64_
     }
     return;
   }
-  const int64_t blo = min(max(off[e], int64_t{0}), nflat);
-  const int64_t bhi = min(max(off[e + 1], blo), nflat);
+  // the expert's row segment, searched in the sorted rhs by every wave (no
+  // offsets pre-pass)
+  const int64_t oe = seg_lower_bound(a.bm.rhs, a.bm.rhs_dt, nflat, a.bm.nw, e, lane);
+  const int64_t oe1 = seg_lower_bound(a.bm.rhs, a.bm.rhs_dt, nflat, a.bm.nw, e + 1, lane);
+  const int64_t blo = min(max(oe, int64_t{0}), nflat);
+  const int64_t bhi = min(max(oe1, blo), nflat);
   if (blo >= bhi) return;  // workgroup-uniform
   const int64_t rows_total = (bhi - blo) * Mx;
   const int gshift = __builtin_ctz(a.gs);
@@ -557,7 +566,7 @@ int gat_cu_count() {
 }
 
 template <int XT, int GB, bool GLU, int S>
-hipError_t gstream_go(const QmmArgs& a, int64_t nflat, int64_t E, const int64_t* off) {
+hipError_t gstream_go(const QmmArgs& a, int64_t nflat, int64_t E) {
   constexpr int NT = GLU ? 2 : 1, D = 3, KB = 4;
   if constexpr (!stream_fits<NT, 1, S, D, KB, GB>()) {
     return hipErrorInvalidValue;
@@ -570,25 +579,25 @@ hipError_t gstream_go(const QmmArgs& a, int64_t nflat, int64_t E, const int64_t*
     const int64_t nblk = (E + 1) * Z;
     if (nblk > 0x7fffffffLL) return hipErrorInvalidConfiguration;
     hipLaunchKernelGGL((gather_stream_kernel<XT, NT, GB, S, D, KB, GLU>), dim3(static_cast<unsigned>(nblk)),
-                       dim3(64 * S), 0, a.stream, a, nflat, off, Z);
+                       dim3(64 * S), 0, a.stream, a, nflat, Z);
     return hipGetLastError();
   }
 }
 
 template <int XT, int GB, bool GLU>
-hipError_t gstream_s(const QmmArgs& a, int64_t nflat, int64_t E, const int64_t* off) {
+hipError_t gstream_s(const QmmArgs& a, int64_t nflat, int64_t E) {
   switch (a.K / 512) {
-    case 1: return gstream_go<XT, GB, GLU, 1>(a, nflat, E, off);
-    case 2: return gstream_go<XT, GB, GLU, 2>(a, nflat, E, off);
-    case 4: return gstream_go<XT, GB, GLU, 4>(a, nflat, E, off);
-    default: return gstream_go<XT, GB, GLU, 8>(a, nflat, E, off);
+    case 1: return gstream_go<XT, GB, GLU, 1>(a, nflat, E);
+    case 2: return gstream_go<XT, GB, GLU, 2>(a, nflat, E);
+    case 4: return gstream_go<XT, GB, GLU, 4>(a, nflat, E);
+    default: return gstream_go<XT, GB, GLU, 8>(a, nflat, E);
   }
 }
 
 template <int XT>
-hipError_t gstream_xt(const QmmArgs& a, int64_t nflat, int64_t E, const int64_t* off) {
-  if (a.gs == 32) return a.glu ? gstream_s<XT, 4, true>(a, nflat, E, off) : gstream_s<XT, 4, false>(a, nflat, E, off);
-  return a.glu ? gstream_s<XT, 2, true>(a, nflat, E, off) : gstream_s<XT, 2, false>(a, nflat, E, off);
+hipError_t gstream_xt(const QmmArgs& a, int64_t nflat, int64_t E) {
+  if (a.gs == 32) return a.glu ? gstream_s<XT, 4, true>(a, nflat, E) : gstream_s<XT, 4, false>(a, nflat, E);
+  return a.glu ? gstream_s<XT, 2, true>(a, nflat, E) : gstream_s<XT, 2, false>(a, nflat, E);
 }
 
 }  // namespace
@@ -600,8 +609,8 @@ bool gather_stream_supported(const QmmArgs& a) {
          (reinterpret_cast<uintptr_t>(a.s) | reinterpret_cast<uintptr_t>(a.b)) % 16 == 0;
 }
 
-hipError_t launch_gather_stream(const QmmArgs& a, int64_t nflat, int64_t E, const int64_t* off) {
-  return a.xdt == BF16 ? gstream_xt<BF16>(a, nflat, E, off) : gstream_xt<F16>(a, nflat, E, off);
+hipError_t launch_gather_stream(const QmmArgs& a, int64_t nflat, int64_t E) {
+  return a.xdt == BF16 ? gstream_xt<BF16>(a, nflat, E) : gstream_xt<F16>(a, nflat, E);
 }
 
 

@@ -1085,6 +1085,16 @@ hipError_t launch_gather_sorted(const QmmArgs& a, int64_t nflat, int64_t E) {
   if (a.xdt != BF16 && a.xdt != F16) return hipErrorInvalidValue;
   if (a.N <= 0 || E <= 0 || nflat <= 0) return hipSuccess;
   if (E + 1 > 65535) return hipErrorInvalidConfiguration;
+  // few rows per expert (at most 8 on average) and K of 1024 or more: the
+  // per-expert streaming kernel, which fetches and converts each pass's x rows
+  // once (256 experts, top 8, T = 64: gate 2048 -> 512 39.5 -> 36.1 us, expert
+  // block 138 -> 125 us) and finds its expert's row segment in the sorted rhs
+  // itself, with no offsets pre-pass (36.1 -> 33.0 us); more rows per expert,
+  // or K = 512, keep the column-block kernel (T = 512: even for the gate, down
+  // 64 -> 75 us), whose many short workgroups read the pre-pass's offsets (the
+  // in-kernel search there: T = 512 down 63 -> 69 us)
+  if (gather_stream_supported(a) && a.K >= 1024 && nflat * a.M <= 8 * E)
+    return launch_gather_stream(a, nflat, E);
   // segment offsets in the stream's offsets workspace (workspace.hip)
   void* ws = nullptr;
   hipError_t e = workspace_get(a.stream, WS_OFFSETS, static_cast<size_t>(E + 1) * sizeof(int64_t), &ws);
@@ -1095,13 +1105,7 @@ hipError_t launch_gather_sorted(const QmmArgs& a, int64_t nflat, int64_t E) {
                      a.bm.rhs_dt, nflat, E, off);
   e = hipGetLastError();
   if (e == hipSuccess) {
-    // few rows per expert (at most 8 on average) and K of 1024 or more: the
-    // per-expert streaming kernel, which fetches and converts each pass's x
-    // rows once (256 experts, top 8, T = 64: gate 2048 -> 512 39.5 -> 36.1 us,
-    // expert block 138 -> 125 us); more rows per expert, or K = 512, keep the
-    // column-block kernel (T = 512: even for the gate, down 64 -> 75 us)
-    if (gather_stream_supported(a) && a.K >= 1024 && nflat * a.M <= 8 * E) e = launch_gather_stream(a, nflat, E, off);
-    else if (gather_decode_supported(a)) e = launch_gather_decode(a, nflat, E, off);
+    if (gather_decode_supported(a)) e = launch_gather_decode(a, nflat, E, off);
     else e = a.xdt == BF16 ? gather_by_mode<BF16>(a, nflat, E, off) : gather_by_mode<F16>(a, nflat, E, off);
   }
   return e;

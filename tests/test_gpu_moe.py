@@ -157,7 +157,8 @@ def test_gather_stream_few_rows_per_expert(ops, H, I, dt):
     1024 or more: the per-expert streaming kernel (K = 1024 / 2048 / 4096:
     two, four and eight waves; a ragged N; one lhs index out of range, whose
     row is NaN).  The product against the oracle's per-row products, and the
-    fused SwiGLU bit-exact against the oracle's SwiGLU of that product."""
+    fused SwiGLU bit-exact against the oracle's SwiGLU of that product;
+    expert indices outside [0, E) give NaN rows."""
     print(f"gather stream H={H} I={I} {dt}", flush=True)
     rng = np.random.default_rng(H + I)
     E, k, T = 64, 8, 40   # 320 rows over 64 experts: 5 per expert
@@ -167,7 +168,10 @@ def test_gather_stream_few_rows_per_expert(ops, H, I, dt):
     ex = torch.from_numpy(np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32))
     flat = ex.reshape(-1)
     order = torch.argsort(flat, stable=True)
-    rhs = flat[order].contiguous().cuda()
+    rhs_h = flat[order].contiguous()
+    rhs_h[:2] = -1       # expert indices outside [0, E) sort first / last: NaN rows
+    rhs_h[-1] = E + 5
+    rhs = rhs_h.cuda()
     lhs_h = (order // k).to(torch.int32)
     lhs_h[7] = T + 3  # out of range: NaN row
     lhs = lhs_h.contiguous().cuda()
@@ -175,19 +179,20 @@ def test_gather_stream_few_rows_per_expert(ops, H, I, dt):
     got = ops.gather_qmm_swiglu(x, w, s, b, lhs, rhs, 64, 4, sorted_indices=True)
     torch.cuda.synchronize()
     g = as_f64(to_np(gu, dt).reshape(T * k, 2 * I), dt)
-    assert np.all(np.isnan(g[7]))
+    bad = [0, 1, 7, T * k - 1]
+    assert np.all(np.isnan(g[bad]))
     ok = np.ones(T * k, bool)
-    ok[7] = False
+    ok[bad] = False
     xs = to_np(x[:, 0], dt)[np.clip(lhs_h.numpy(), 0, T - 1)]
     rn = rhs.cpu().numpy()
     refp = np.zeros((T * k, 2 * I))
-    for e in np.unique(rn):
-        rows = np.nonzero(rn == e)[0]
+    for e in np.unique(rn[ok]):
+        rows = np.nonzero((rn == e) & ok)[0]
         refp[rows] = oracle.qmv_affine(xs[rows], dt, wn[e], sn[e], bn[e], dt, 64, 4, odt="f32", nthreads=8)
     assert rel_err(g[ok], refp[ok]) <= 1e-2
     ref = oracle.swiglu(to_np(gu, dt).reshape(T * k, 2 * I)[ok], dt)
     assert np.array_equal(_bits(got, dt).reshape(T * k, I)[ok], np.ascontiguousarray(ref).view(np.uint16))
-    assert np.all(np.isnan(as_f64(to_np(got, dt), dt).reshape(T * k, I)[7]))
+    assert np.all(np.isnan(as_f64(to_np(got, dt), dt).reshape(T * k, I)[bad]))
 
 
 # ------------------------------------------------------------------ row gather
