@@ -1,8 +1,10 @@
 // convert.hip — dequantize and quantize on the GPU.
 //
 // dequantize (mlx/src/ops.rs:653-686; caller mlx/src/nn/embedding.rs:62-72):
-//   one thread per 32-code chunk: `bits` words in, 32 values out, bit-exact;
-//   with an index array, output row i is table row idx[i] (the embedding
+//   one thread per packed word (dequant_words_kernel: 2 / 4 / 8-bit codes and
+//   the fp modes, rows of whole 32-code chunks) or per 32-code chunk
+//   (dequant_kernel: 3 / 5 / 6-bit codes and other rows), bit-exact either
+//   way; with an index array, output row i is table row idx[i] (the embedding
 //   lookup without dequantizing the whole table):
 //   affine  v = rn(rn(s * q) + b)  (multiply and add rounded separately),
 //   fp      v = rn(elem(q) * scale), then RNE to the output dtype.

@@ -1,5 +1,8 @@
 // qmm_gather.hip — sorted grouped gather_qmm (affine 4-bit, gs 32 / 64 / 128)
-// with the factored MFMA arithmetic of qmm_decode.hip.
+// with the factored MFMA arithmetic of qmm_decode.hip: gather_decode_kernel
+// (one 64-column block of one expert per workgroup) and gather_stream_kernel
+// (few rows per expert: each expert's weights streamed past x rows fetched
+// once per pass).
 #include <algorithm>
 #include <type_traits>
 

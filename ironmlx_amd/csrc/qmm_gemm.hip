@@ -11,6 +11,8 @@
 //   - eight-wave DMA kernel (other transposed shapes): dequantized W shared
 //     through an LDS ring;
 //   - register-staged kernel (transpose = false).
+// Affine 2 / 3 / 5 / 6-bit codes of one weight matrix are first widened to 4 /
+// 8-bit codes (widen_codes_kernel) and take the register-B kernel.
 // Dequantization uses the arithmetic of `dequantize` (s * q + b, or the fp
 // element times its scale) rounded once to x's 16-bit type.
 
