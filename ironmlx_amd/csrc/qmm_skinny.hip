@@ -1085,16 +1085,17 @@ hipError_t launch_gather_sorted(const QmmArgs& a, int64_t nflat, int64_t E) {
   if (a.xdt != BF16 && a.xdt != F16) return hipErrorInvalidValue;
   if (a.N <= 0 || E <= 0 || nflat <= 0) return hipSuccess;
   if (E + 1 > 65535) return hipErrorInvalidConfiguration;
-  // K of 1024 or more (affine 4-bit, gs 64): the per-expert streaming kernel,
-  // which fetches and converts each pass's x rows once and streams the
-  // expert's weights past them, finding its row segment in the sorted rhs
-  // itself (no offsets pre-pass).  256 experts, top 8: T = 64 gate 2048 -> 512
-  // 39.5 -> 32.8 us, T = 512 gate 62-63 -> 60.7 us, fused gate_up expert block
-  // T = 64 / 512: 138 / 213 -> 119 / 199 us.  K = 512 (the down projection)
-  // keeps the column-block kernel (streamed: T = 512 64 -> 75 us), whose many
-  // short workgroups read the pre-pass's offsets (an in-kernel search there:
-  // 63 -> 69 us).
-  if (gather_stream_supported(a) && a.K >= 1024) return launch_gather_stream(a, nflat, E);
+  // K of 1024 or more (affine 4-bit, gs 64), or few rows per expert (at most
+  // 8 on average): the per-expert streaming kernel, which fetches and converts
+  // each pass's x rows once and streams the expert's weights past them,
+  // finding its row segment in the sorted rhs itself (no offsets pre-pass).
+  // 256 experts, top 8: T = 64 gate 2048 -> 512 39.5 -> 32.8 us, down
+  // 512 -> 2048 38.3 -> 35.3 us; T = 512 gate 62-63 -> 60.1 us; fused gate_up
+  // expert block T = 64 / 512: 138 / 213 -> 119 / 199 us.  The T = 512 down
+  // projection (K = 512, 16 rows per expert) keeps the column-block kernel
+  // (streamed: 62 -> 68 us), whose many short workgroups read the pre-pass's
+  // offsets (an in-kernel search there: 63 -> 69 us).
+  if (gather_stream_supported(a) && (a.K >= 1024 || nflat * a.M <= 8 * E)) return launch_gather_stream(a, nflat, E);
   // segment offsets in the stream's offsets workspace (workspace.hip)
   void* ws = nullptr;
   hipError_t e = workspace_get(a.stream, WS_OFFSETS, static_cast<size_t>(E + 1) * sizeof(int64_t), &ws);
