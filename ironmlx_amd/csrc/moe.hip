@@ -326,7 +326,10 @@ __global__ __launch_bounds__(SORT_BLOCK) void moe_scatter_kernel(const int32_t* 
 // once (in LDS), then each thread runs the ordered sum for its column
 // (blockIdx.y picks 256 columns).  Rows may be in any order in y (sorted by
 // expert, or one row per (token, slot) when the sort is skipped).
-template <int DT>
+// VEC > 1: each thread takes VEC consecutive columns (one 16-byte load per
+// row, D % VEC == 0), so a token's rows are read in full 16-byte pieces and
+// the ranking is paid once per 256 VEC columns.
+template <int DT, int VEC = 1>
 __global__ __launch_bounds__(256) void moe_combine_kernel(const typename Store<DT>::T* y, const int32_t* inverse,
                                                           const int32_t* experts, const float* scores, float* out,
                                                           int T, int k, int64_t D, int E, int64_t n) {
@@ -359,6 +362,42 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const typename Store<D
     }
     __syncthreads();
     const int nv = nvalid;
+    if constexpr (VEC > 1) {
+      using S = typename Store<DT>::T;
+      const int64_t d0 = (static_cast<int64_t>(blockIdx.y) * 256 + tid) * VEC;
+      if (d0 < D) {
+        float acc[VEC];
+#pragma unroll
+        for (int c = 0; c < VEC; ++c) acc[c] = 0.f;
+        for (int i0 = 0; i0 < nv; i0 += 4) {
+          // the loads of up to 4 rows are issued before the ordered adds
+          uint4 v[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            v[j] = i0 + j < nv ? *reinterpret_cast<const uint4*>(y + rowoff[i0 + j] + d0) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            if (i0 + j < nv) {
+              const uint32_t w4[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+              for (int c = 0; c < VEC; ++c) {
+                float e;
+                if constexpr (sizeof(S) == 4) e = __uint_as_float(w4[c]);
+                else e = to_f<DT>(static_cast<S>(w4[c / 2] >> (16 * (c & 1))));
+                const float p = e * wt[i0 + j];
+                acc[c] = i0 + j == 0 ? p : acc[c] + p;
+              }
+            }
+          }
+        }
+        float* o = out + static_cast<int64_t>(t) * D + d0;
+#pragma unroll
+        for (int c = 0; c < VEC; c += 4)
+          *reinterpret_cast<float4*>(o + c) = make_float4(acc[c], acc[c + 1], acc[c + 2], acc[c + 3]);
+      }
+      __syncthreads();
+      continue;
+    }
     const int64_t d = static_cast<int64_t>(blockIdx.y) * 256 + tid;
     if (d < D) {
       float acc = 0.f;
@@ -735,6 +774,28 @@ hipError_t launch_moe_combine(const void* y, int dt, const int32_t* inverse, con
   if (T == 0 || D == 0) return hipSuccess;
   if ((D + 255) / 256 > 65535) return hipErrorInvalidConfiguration;
   const dim3 grid(static_cast<unsigned>(T < 1048576 ? T : 1048576), static_cast<unsigned>((D + 255) / 256));
+  // 16-byte column pieces when every row starts 16-byte aligned (256-expert
+  // top-8 block, D = 2048: T = 512 block 199 -> 194 us, T = 1 18.7 -> 18.0 us)
+  const int vec = dt == F32 ? 4 : 8;
+  if (D % vec == 0 && (reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(out)) % 16 == 0) {
+    const dim3 gv(grid.x, static_cast<unsigned>((D / vec + 255) / 256));
+    switch (dt) {
+      case F32:
+        hipLaunchKernelGGL((moe_combine_kernel<F32, 4>), gv, dim3(256), 0, st, static_cast<const float*>(y), inverse,
+                           experts, scores, out, T, k, D, E, n);
+        return hipGetLastError();
+      case F16:
+        hipLaunchKernelGGL((moe_combine_kernel<F16, 8>), gv, dim3(256), 0, st, static_cast<const uint16_t*>(y),
+                           inverse, experts, scores, out, T, k, D, E, n);
+        return hipGetLastError();
+      case BF16:
+        hipLaunchKernelGGL((moe_combine_kernel<BF16, 8>), gv, dim3(256), 0, st, static_cast<const uint16_t*>(y),
+                           inverse, experts, scores, out, T, k, D, E, n);
+        return hipGetLastError();
+      default:
+        return hipErrorInvalidValue;
+    }
+  }
   switch (dt) {
     case F32:
       hipLaunchKernelGGL(moe_combine_kernel<F32>, grid, dim3(256), 0, st, static_cast<const float*>(y), inverse,

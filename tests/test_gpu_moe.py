@@ -264,7 +264,7 @@ def test_moe_sort_limits(ops):
 
 
 @pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
-@pytest.mark.parametrize("T,k,E,D", [(1, 8, 256, 2048), (64, 8, 256, 2048), (300, 4, 60, 1000)])
+@pytest.mark.parametrize("T,k,E,D", [(1, 8, 256, 2048), (64, 8, 256, 2048), (300, 4, 60, 1000), (5, 3, 17, 1001)])
 def test_moe_combine_bit_exact(ops, dt, T, k, E, D):
     rng = np.random.default_rng(T + D)
     lg = oracle.from_float(rng.standard_normal((T, E)).astype(np.float32), dt)
