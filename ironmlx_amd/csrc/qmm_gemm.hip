@@ -1048,7 +1048,7 @@ hipError_t wr_launch_tile(const QmmArgs& a, int ks, float* part) {
 
 // Tile / split choice for the register-B kernel: 256 x 256 tiles while they
 // give most CUs a tile; otherwise 128 x 128 tiles with K split over enough
-// workgroups to fill the GPU.  Split partials are fp32 in the stream's
+// workgroups to fill the GPU (two per CU when the tiles alone are 128-256).  Split partials are fp32 in the stream's
 // split-K workspace (workspace.hip), summed in a fixed order by
 // splitk_reduce_kernel, so results do not depend on scheduling.
 template <int XT, int MODE, int BITS>
@@ -1061,6 +1061,10 @@ hipError_t wr_launch(const QmmArgs& a, int G) {
   const int span = std::max(128, (MODE == AFFINE ? 8 : 16) * gs);
   int ks = 1;
   while (small * ks < 256 && ks < 16 && a.K % (span * ks * 2) == 0 && a.K / (ks * 2) >= 512) ks *= 2;
+  // Exactly one workgroup per CU from >= 128 tiles: one more split puts two
+  // on each CU, which measured 8-10% faster at K = N = 4096 for M = 512 and
+  // M = 1024 (at M <= 256 and at 1.5 per CU the extra split measured slower).
+  if (small >= 128 && small * ks == 256 && ks < 16 && a.K % (span * ks * 2) == 0 && a.K / (ks * 2) >= 512) ks *= 2;
   (void)G;
   if (ks == 1) return wr_launch_tile<XT, MODE, BITS, 128, 128>(a, 1, nullptr);
   return splitk_run<XT>(a, ks, [&](float* part) { return wr_launch_tile<XT, MODE, BITS, 128, 128>(a, ks, part); });
