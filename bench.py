@@ -132,9 +132,11 @@ def bench_prefill(ops, steps, warmup, M=2048, N=14336, K=4096):
             outs[i] = ops.quantized_matmul(x, w, s, b, True, 64, 4, "affine")
 
     run()
-    torch.cuda.synchronize()
+    # split-K shapes keep fp32 partials in the capture stream's workspace,
+    # sized by an eager pass on it (nothing is allocated while capturing)
+    _warm_on_capture_stream(run)
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+    with torch.cuda.graph(g, stream=_capture_stream()):
         run()
     for _ in range(max(1, warmup)):
         g.replay()

@@ -200,6 +200,29 @@ def test_qmm_split_k_tiles(ops, mode, bits, gs, M, xdt):
     assert rel_err(got, ref) <= tol[xdt]
 
 
+@pytest.mark.parametrize("mode,bits,gs,xdt", [("affine", 4, 64, "bf16"), ("affine", 4, 128, "f16"),
+                                               ("affine", 8, 32, "bf16"), ("affine", 3, 64, "bf16"),
+                                               ("mxfp4", None, None, "bf16"), ("nvfp4", None, None, "f16"),
+                                               ("mxfp8", None, None, "bf16")])
+def test_qmm_big_tiles_split_k(ops, mode, bits, gs, xdt):
+    # 96 output tiles of 256 x 256 over K = 8192: two K halves of the big
+    # tiles, fp32 partials summed in a second pass.  Too large for the CPU
+    # oracle in seconds, so the reference is the library's dequantize (bit
+    # exact against the oracle in the dequantize tests) times x in fp32.
+    M, N, K = 768, 8192, 8192
+    print(f"big-tile split-K {mode} bits={bits} gs={gs} {xdt} M={M} N={N} K={K}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(11)
+    dt = TDT[xdt]
+    wf = (torch.randn((N, K), generator=g, device="cuda") * 0.02).to(dt)
+    wq, s, b = ops.quantize(wf, gs, bits, mode)
+    del wf
+    x = torch.randn((M, K), generator=g, device="cuda").to(dt)
+    got = ops.quantized_matmul(x, wq, s, b, True, gs, bits, mode).float()
+    ref = x.float() @ ops.dequantize(wq, s, b, gs, bits, mode, dtype=dt).float().t()
+    err = ((got - ref).abs().max() / ref.abs().max()).item()
+    assert err <= (TOL if mode == "affine" else TOL_FP)[xdt]
+
+
 @pytest.mark.parametrize("xdt", ["bf16", "f16"])
 @pytest.mark.parametrize("N,K", [(200, 512), (6144, 1024), (8200, 1152)])
 @pytest.mark.parametrize("gs", [32, 64, 128])
