@@ -1057,7 +1057,7 @@ hipError_t wr_launch_tile(const QmmArgs& a, int ks, float* part) {
 }
 
 // Tile / split choice for the register-B kernel: 256 x 256 tiles while they
-// give most CUs a tile (split in two K halves from 96 tiles at K >= 8192);
+// give most CUs a tile (K split in two or four from 64 tiles at K >= 8192);
 // otherwise 128 x 128 tiles with K split over enough
 // workgroups to fill the GPU (two per CU when the tiles alone are 128-256).  Split partials are fp32 in the stream's
 // split-K workspace (workspace.hip), summed in a fixed order by
@@ -1069,12 +1069,16 @@ hipError_t wr_launch(const QmmArgs& a, int G) {
   // each split keeps whole scale chunks (8 or 16 groups) and 128-code W chunks
   const int gs = MODE == AFFINE ? a.gs : ModeInfo<MODE>::GS;
   const int span = std::max(128, (MODE == AFFINE ? 8 : 16) * gs);
-  // 96-191 big tiles over long K: two K halves of 256 x 256 tiles (the fp32
-  // partial round trip is small next to K >= 8192 of MFMA work; M = 2048,
-  // K = 14336, N = 4096 measured 311 -> 264-276 us against 128 x 128 tiles,
-  // while at K = 4096 the split measured slower)
-  if (big >= 96 && a.K % (span * 2) == 0 && a.K >= 8192)
-    return splitk_run<XT>(a, 2, [&](float* part) { return wr_launch_tile<XT, MODE, BITS, 256, 256>(a, 2, part); });
+  // 64-191 big tiles over long K: two (96-191) or four (64-95) K ranges of
+  // 256 x 256 tiles (the fp32 partial round trip is small next to K >= 8192
+  // of MFMA work; against 128 x 128 tiles M = 2048, K = 14336, N = 4096
+  // measured 311 -> 264-276 us and M = 1024 159 -> 145 us, while at K = 4096
+  // the split measured slower)
+  if (big >= 64 && a.K >= 8192) {
+    const int kb = big >= 96 ? 2 : 4;
+    if (a.K % (span * kb) == 0)
+      return splitk_run<XT>(a, kb, [&](float* part) { return wr_launch_tile<XT, MODE, BITS, 256, 256>(a, kb, part); });
+  }
   const int64_t small = ((a.M + 127) / 128) * ((a.N + 127) / 128) * a.nbatch;
   int ks = 1;
   while (small * ks < 256 && ks < 16 && a.K % (span * ks * 2) == 0 && a.K / (ks * 2) >= 512) ks *= 2;

@@ -204,12 +204,14 @@ def test_qmm_split_k_tiles(ops, mode, bits, gs, M, xdt):
                                                ("affine", 8, 32, "bf16"), ("affine", 3, 64, "bf16"),
                                                ("mxfp4", None, None, "bf16"), ("nvfp4", None, None, "f16"),
                                                ("mxfp8", None, None, "bf16")])
-def test_qmm_big_tiles_split_k(ops, mode, bits, gs, xdt):
-    # 96 output tiles of 256 x 256 over K = 8192: two K halves of the big
-    # tiles, fp32 partials summed in a second pass.  Too large for the CPU
-    # oracle in seconds, so the reference is the library's dequantize (bit
-    # exact against the oracle in the dequantize tests) times x in fp32.
-    M, N, K = 768, 8192, 8192
+@pytest.mark.parametrize("M", [768, 512])
+def test_qmm_big_tiles_split_k(ops, mode, bits, gs, xdt, M):
+    # 96 (M = 768) or 64 (M = 512) output tiles of 256 x 256 over K = 8192:
+    # two or four K ranges of the big tiles, fp32 partials summed in a second
+    # pass.  Too large for the CPU oracle in seconds, so the reference is the
+    # library's dequantize (bit exact against the oracle in the dequantize
+    # tests) times x in fp32.
+    N, K = 8192, 8192
     print(f"big-tile split-K {mode} bits={bits} gs={gs} {xdt} M={M} N={N} K={K}", flush=True)
     g = torch.Generator(device="cuda").manual_seed(11)
     dt = TDT[xdt]
